@@ -1,0 +1,88 @@
+// Shared device helpers for the MoE HIP kernels (gfx950 / CDNA4).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef uint16_t bf16_t;  // bfloat16 storage
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+#define MOE_DEV __device__ __forceinline__
+
+MOE_DEV float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
+
+// float -> bfloat16, round to nearest even; NaN stays NaN.
+MOE_DEV bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+
+// Elements of T in one 16-byte vector.
+template <typename T> struct Vec16;
+template <> struct Vec16<bf16_t> { static constexpr int N = 8; };
+template <> struct Vec16<float> { static constexpr int N = 4; };
+
+template <typename T> MOE_DEV float to_f(T v);
+template <> MOE_DEV float to_f<float>(float v) { return v; }
+template <> MOE_DEV float to_f<bf16_t>(bf16_t v) { return bf2f(v); }
+template <typename T> MOE_DEV T from_f(float v);
+template <> MOE_DEV float from_f<float>(float v) { return v; }
+template <> MOE_DEV bf16_t from_f<bf16_t>(float v) { return f2bf(v); }
+
+// 16-byte vector <-> floats
+MOE_DEV void unpack16(u32x4 v, float* f, bf16_t) {
+  uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f[2 * i] = __uint_as_float(w[i] << 16);
+    f[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+MOE_DEV void unpack16(u32x4 v, float* f, float) {
+  f[0] = __uint_as_float(v.x); f[1] = __uint_as_float(v.y);
+  f[2] = __uint_as_float(v.z); f[3] = __uint_as_float(v.w);
+}
+MOE_DEV u32x4 pack16(const float* f, bf16_t) {
+  u32x4 r;
+  r.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
+  r.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
+  r.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
+  r.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+  return r;
+}
+MOE_DEV u32x4 pack16(const float* f, float) {
+  u32x4 r;
+  r.x = __float_as_uint(f[0]); r.y = __float_as_uint(f[1]);
+  r.z = __float_as_uint(f[2]); r.w = __float_as_uint(f[3]);
+  return r;
+}
+
+template <typename T> MOE_DEV u32x4 ld16(const T* p) { return *reinterpret_cast<const u32x4*>(p); }
+template <typename T> MOE_DEV void st16(T* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+MOE_DEV float silu_f(float g) { return g / (1.0f + __expf(-g)); }
+MOE_DEV float sigmoid_f(float g) { return 1.0f / (1.0f + __expf(-g)); }
+
+// Wave-wide (64 lanes) butterfly reductions: fixed order, so bit-reproducible.
+MOE_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+MOE_DEV float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Map a linear workgroup id so that the blocks one XCD receives (ids are
+// dealt round-robin over the 8 XCDs) form one contiguous range of logical
+// tiles: neighbouring tiles then share that XCD's L2.
+MOE_DEV int xcd_remap(int id, int n) {
+  const int x = id & 7, q = n >> 3, r = n & 7;
+  return x * q + (x < r ? x : r) + (id >> 3);
+}

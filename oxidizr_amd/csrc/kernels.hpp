@@ -1,0 +1,734 @@
+// HIP kernels of the MoE layer forward and backward (gfx950 / CDNA4).
+//
+// Semantics restate oxidizr's MoE layer (reference src/model.rs:1385-1958,
+// arithmetic of boostr::nn::moe with explicit constants):
+//   logits = x Wr^T (+ b);  probs = softmax(logits / tau);  top-k on logits,
+//   lowest expert index first on ties;  w = probs[top-k] (optionally renormalised);
+//   per expert: G = X Wg^T, U = X Wu^T, A = silu(G) * U, Y = A Wd^T;
+//   out_t = sum_j w_tj Y[pos(t, j)] + s * shared(x_t);
+//   aux = E (c_sw sum_e f_e P_e + c_sq sum_e P_e^2), z = mean_t lse_t^2.
+// No floating-point atomics anywhere; integer LDS atomics only in the
+// expert histogram, whose result is order-independent.
+#pragma once
+#include <climits>
+#include <cmath>
+#include "gemm.hpp"
+
+namespace moe {
+
+// ------------------------------------------------------------------ tilings
+template <typename T> struct GemmTiling;
+template <> struct GemmTiling<bf16_t> { using C = Tiling<bf16_t, 128, 128, 64>; };
+template <> struct GemmTiling<float> { using C = Tiling<float, 128, 128, 32>; };
+
+// Row-grouped problems: groups split the M dimension (permuted token rows).
+// offsets == nullptr means one dense group of M rows.
+struct RowGroups {
+  const int* offsets;      // [G + 1] row offsets
+  const int* tile_prefix;  // [G + 1] prefix of ceil(count / BM)
+  int G;
+  int M;
+};
+
+MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, int& row0,
+                          int& mv, int& n0) {
+  const int nN = (N + BN - 1) / BN;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  const int mt = id / nN, nt = id % nN;
+  n0 = nt * BN;
+  if (g.offsets == nullptr) {
+    grp = 0;
+    row0 = mt * BM;
+    mv = min(BM, g.M - row0);
+    return mv > 0;
+  }
+  if (mt >= g.tile_prefix[g.G]) return false;
+  grp = find_group(g.tile_prefix, g.G, mt);
+  const int local = (mt - g.tile_prefix[grp]) * BM;
+  row0 = g.offsets[grp] + local;
+  mv = min(BM, g.offsets[grp + 1] - g.offsets[grp] - local);
+  return mv > 0;
+}
+
+// K-grouped problems (weight gradients): groups split the reduction over
+// token rows.  offsets == nullptr means one group with K rows.
+struct KGroups {
+  const int* offsets;
+  int G;
+  int K;
+};
+
+MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& krow0,
+                       int& K, int& m0, int& n0) {
+  const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+  const int per = nM * nN;
+  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  grp = id / per;
+  const int r = id % per;
+  m0 = (r / nN) * BM;
+  n0 = (r % nN) * BN;
+  if (grp >= g.G) return false;
+  if (g.offsets) {
+    krow0 = g.offsets[grp];
+    K = g.offsets[grp + 1] - krow0;
+  } else {
+    krow0 = 0;
+    K = g.K;
+  }
+  return K > 0;
+}
+
+template <typename T>
+MOE_DEV const T* pick(const T* const* tab, const T* single, int g) {
+  return tab ? tab[g] : single;
+}
+template <typename T>
+MOE_DEV T* pick(T* const* tab, T* single, int g) {
+  return tab ? tab[g] : single;
+}
+
+// ------------------------------------------------------------------ router GEMM
+// logits[t, e] = x[t] . Wr[e] (+ bias[e]), fp32 out.
+template <typename T>
+__global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
+                                                       const T* __restrict__ wr,
+                                                       const float* __restrict__ bias,
+                                                       float* __restrict__ logits, int Tn, int H,
+                                                       int E) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  RowGroups g{nullptr, nullptr, 1, Tn};
+  int grp, row0, mv, n0;
+  if (!resolve_rows(g, E, C::BM, C::BN, grp, row0, mv, n0)) return;
+  OpDesc<T> a[1] = {{x + (int64_t)row0 * H, H, mv, H}};
+  OpDesc<T> b[1] = {{wr + (int64_t)n0 * H, H, E - n0, H}};
+  f32x16 acc[1][C::TN][C::TM];
+  zero_acc<C, 1>(acc);
+  mainloop<C, T, false, false, 1, 1>(acc, a, b, H, smem);
+  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = n0 + n + i;
+      if (e < E) logits[(int64_t)(row0 + m) * E + e] = v[0][i] + (bias ? bias[e] : 0.0f);
+    }
+  });
+}
+
+// ------------------------------------------------------------------ routing
+// One wave per token: softmax(logits / tau), log-sum-exp, top-k on the raw
+// logits (NaN selects as -inf; equal values -> lower expert index first).
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int Tn, int E,
+                                               int k, float tau, int norm,
+                                               float* __restrict__ probs, float* __restrict__ lse,
+                                               int* __restrict__ idx, float* __restrict__ w) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const float* row = logits + (int64_t)t * E;
+  float v[EPL], ex[EPL];
+  float mx = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    v[i] = e < E ? row[e] : -INFINITY;
+    if (e < E) mx = fmaxf(mx, v[i] / tau);
+  }
+  mx = wave_max(mx);
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    ex[i] = e < E ? expf(v[i] / tau - mx) : 0.0f;
+    s += ex[i];
+  }
+  s = wave_sum(s);
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) probs[(int64_t)t * E + e] = ex[i] / s;
+  }
+  if (lane == 0) lse[t] = mx + logf(s);
+
+  uint32_t taken = 0;
+  float wsel[16];
+  int isel[16];
+  float wsum = 0.0f;
+  for (int j = 0; j < k; ++j) {
+    float bv = -INFINITY;
+    int be = INT_MAX;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      const float val = isnan(v[i]) ? -INFINITY : v[i];
+      if (e < E && !((taken >> i) & 1u) && (be == INT_MAX || val > bv)) {
+        bv = val;
+        be = e;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+      const float ov = __shfl_xor(bv, o, 64);
+      const int oe = __shfl_xor(be, o, 64);
+      const bool better = oe != INT_MAX && (be == INT_MAX || ov > bv || (ov == bv && oe < be));
+      if (better) {
+        bv = ov;
+        be = oe;
+      }
+    }
+    // every lane now holds the same winner; its owner marks it taken
+    float mine = 0.0f;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i == be) {
+        taken |= 1u << i;
+        mine = ex[i];
+      }
+    const float pj = __shfl(mine, be & 63, 64) / s;
+    wsel[j] = pj;
+    isel[j] = be;
+    wsum += pj;
+  }
+  if (lane == 0) {
+    for (int j = 0; j < k; ++j) {
+      idx[(int64_t)t * k + j] = isel[j];
+      w[(int64_t)t * k + j] = norm ? wsel[j] / wsum : wsel[j];
+    }
+  }
+}
+
+// ------------------------------------------------------------------ column sums
+// part[rb, e] = sum over rows [rb*64, rb*64+64) of a[t, e], fixed order.
+__global__ __launch_bounds__(256) void k_colsum_partial(const float* __restrict__ a, int Tn, int E,
+                                                        float* __restrict__ part) {
+  __shared__ float red[4][64];
+  const int c = threadIdx.x & 63, r = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + c;
+  const int t0 = blockIdx.y * 64;
+  float s = 0.0f;
+  if (e < E)
+    for (int t = t0 + r; t < min(t0 + 64, Tn); t += 4) s += a[(int64_t)t * E + e];
+  red[r][c] = s;
+  __syncthreads();
+  if (r == 0 && e < E)
+    part[(int64_t)blockIdx.y * E + e] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
+}
+
+// out[e] = scale * sum_rb part[rb, e], rb ascending.
+__global__ void k_colsum_final(const float* __restrict__ part, int nrb, int E, float scale,
+                               float* __restrict__ out) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= E) return;
+  float s = 0.0f;
+  for (int rb = 0; rb < nrb; ++rb) s += part[(int64_t)rb * E + e];
+  out[e] = s * scale;
+}
+
+// aux = E (c_sw sum_e f_e P_e + c_sq sum_e P_e^2), z = mean_t lse_t^2.
+__global__ __launch_bounds__(256) void k_losses(const float* __restrict__ P,
+                                                const int* __restrict__ counts,
+                                                const float* __restrict__ lse, int Tn, int E,
+                                                int k, float c_sw, float c_sq,
+                                                float* __restrict__ aux, float* __restrict__ z) {
+  __shared__ float r_sw[256], r_sq[256], r_z[256];
+  const int tid = threadIdx.x;
+  const float inv_tk = 1.0f / ((float)Tn * (float)k);
+  float sw = 0.0f, sq = 0.0f, zz = 0.0f;
+  for (int e = tid; e < E; e += 256) {
+    const float p = P[e];
+    sw += ((float)counts[e] * inv_tk) * p;
+    sq += p * p;
+  }
+  for (int t = tid; t < Tn; t += 256) zz += lse[t] * lse[t];
+  r_sw[tid] = sw; r_sq[tid] = sq; r_z[tid] = zz;
+  __syncthreads();
+  for (int o = 128; o >= 1; o >>= 1) {
+    if (tid < o) {
+      r_sw[tid] += r_sw[tid + o];
+      r_sq[tid] += r_sq[tid + o];
+      r_z[tid] += r_z[tid + o];
+    }
+    __syncthreads();
+  }
+  if (tid == 0) {
+    if (aux) *aux = (float)E * (c_sw * r_sw[0] + c_sq * r_sq[0]);
+    if (z) *z = r_z[0] / (float)Tn;
+  }
+}
+
+// ------------------------------------------------------------------ dispatch
+// Per-block expert histogram of 256 tokens' k assignments.
+__global__ __launch_bounds__(256) void k_hist(const int* __restrict__ idx, int Tn, int k, int E,
+                                              int* __restrict__ block_hist) {
+  extern __shared__ int hist[];
+  for (int e = threadIdx.x; e < E; e += 256) hist[e] = 0;
+  __syncthreads();
+  const int t = blockIdx.x * 256 + threadIdx.x;
+  if (t < Tn)
+    for (int j = 0; j < k; ++j) atomicAdd(&hist[idx[(int64_t)t * k + j]], 1);
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += 256) block_hist[(int64_t)blockIdx.x * E + e] = hist[e];
+}
+
+// counts, exclusive offsets, per-block bases, and GEMM tile prefixes for the
+// row-tile heights in kTileBM.
+constexpr int kNumTileBM = 5;
+__constant__ int kTileBM[kNumTileBM] = {16, 32, 64, 128, 256};
+
+__global__ __launch_bounds__(256) void k_scan(const int* __restrict__ block_hist, int nb, int E,
+                                              int* __restrict__ block_base,
+                                              int* __restrict__ counts,
+                                              int* __restrict__ offsets,
+                                              int* __restrict__ tile_prefix) {
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    int run = 0;
+    for (int b = 0; b < nb; ++b) {
+      const int c = block_hist[(int64_t)b * E + e];
+      block_base[(int64_t)b * E + e] = run;
+      run += c;
+    }
+    counts[e] = run;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int run = 0;
+    offsets[0] = 0;
+    for (int e = 0; e < E; ++e) {
+      run += counts[e];
+      offsets[e + 1] = run;
+    }
+  }
+  if (threadIdx.x >= 32 && threadIdx.x < 32 + kNumTileBM) {
+    const int j = threadIdx.x - 32, bm = kTileBM[j];
+    int* tp = tile_prefix + j * (E + 1);
+    int run = 0;
+    tp[0] = 0;
+    for (int e = 0; e < E; ++e) {
+      run += (counts[e] + bm - 1) / bm;
+      tp[e + 1] = run;
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+    const int base = offsets[e];
+    for (int b = 0; b < nb; ++b) block_base[(int64_t)b * E + e] += base;
+  }
+}
+
+// Stable scatter: position of assignment (t, j) = offset of its expert +
+// number of earlier tokens (same expert) before it.  Ranks inside a wave come
+// from ballots that match expert ids bit by bit; across the block's 4 waves
+// from per-wave counts.
+__global__ __launch_bounds__(256) void k_scatter(const int* __restrict__ idx, int Tn, int k,
+                                                 int E, int nbits,
+                                                 const int* __restrict__ block_base,
+                                                 int* __restrict__ perm,
+                                                 int* __restrict__ inv_perm) {
+  extern __shared__ int lds[];
+  int* wcnt = lds;            // [4][E]
+  int* wbase = lds + 4 * E;   // [4][E]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int t = blockIdx.x * 256 + tid;
+  const bool valid = t < Tn;
+  for (int i = tid; i < 4 * E; i += 256) wcnt[i] = 0;
+  __syncthreads();
+  int keys[16];
+  for (int j = 0; j < k; ++j) {
+    keys[j] = valid ? idx[(int64_t)t * k + j] : E;
+    if (valid) atomicAdd(&wcnt[wave * E + keys[j]], 1);
+  }
+  __syncthreads();
+  for (int e = tid; e < E; e += 256) {
+    int s = 0;
+    for (int w = 0; w < 4; ++w) {
+      wbase[w * E + e] = s;
+      s += wcnt[w * E + e];
+    }
+  }
+  __syncthreads();
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  for (int j = 0; j < k; ++j) {
+    const int e = keys[j];
+    uint64_t uni = 0;
+    for (int j2 = 0; j2 < k; ++j2) {
+      uint64_t m = ~0ull;
+      for (int bit = 0; bit < nbits; ++bit) {
+        const uint64_t bal = __ballot((keys[j2] >> bit) & 1);
+        m &= ((e >> bit) & 1) ? bal : ~bal;
+      }
+      uni |= m;
+    }
+    const int rank = __popcll(uni & below);
+    if (valid) {
+      const int pos = block_base[(int64_t)blockIdx.x * E + e] + wbase[wave * E + e] + rank;
+      perm[pos] = t * k + j;
+      inv_perm[(int64_t)t * k + j] = pos;
+    }
+  }
+}
+
+// x_perm[pos] = x[perm[pos] / k]; one wave per row, 16-byte vectors.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
+                                                const int* __restrict__ perm, int Tn, int k,
+                                                int H, T* __restrict__ xp) {
+  constexpr int V = Vec16<T>::N;
+  const int64_t TK = (int64_t)Tn * k;
+  const int64_t pos = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (pos >= TK) return;
+  const int lane = threadIdx.x & 63;
+  int tok = perm[pos] / k;
+  tok = tok < 0 ? 0 : (tok >= Tn ? Tn - 1 : tok);
+  const T* src = x + (int64_t)tok * H;
+  T* dst = xp + pos * H;
+  for (int c = lane; c < H / V; c += 64) st16(dst + c * V, ld16(src + c * V));
+}
+
+// ------------------------------------------------------------------ expert GEMMs (forward)
+// G = X Wg^T, U = X Wu^T, A = silu(G) * U for each row group (expert), or for
+// all T rows (shared expert, groups.offsets == nullptr).
+template <typename T>
+__global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
+                                                    const T* const* wg_tab, const T* wg_one,
+                                                    const T* const* wu_tab, const T* wu_one,
+                                                    int H, int N, T* __restrict__ G,
+                                                    T* __restrict__ U, T* __restrict__ A) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, 1, 2>()];
+  int grp, row0, mv, n0;
+  if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
+  const T* wg = pick(wg_tab, wg_one, grp);
+  const T* wu = pick(wu_tab, wu_one, grp);
+  OpDesc<T> a[1] = {{X + (int64_t)row0 * H, H, mv, H}};
+  OpDesc<T> b[2] = {{wg + (int64_t)n0 * H, H, N - n0, H}, {wu + (int64_t)n0 * H, H, N - n0, H}};
+  f32x16 acc[2][C::TN][C::TM];
+  zero_acc<C, 2>(acc);
+  mainloop<C, T, false, false, 1, 2>(acc, a, b, H, smem);
+  for_each_frag<C, 2>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv || n0 + n >= N) return;
+    float act[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) act[i] = silu_f(v[0][i]) * v[1][i];
+    const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
+    store4(G + o, v[0]);
+    store4(U + o, v[1]);
+    store4(A + o, act);
+  });
+}
+
+// Y = A Wd^T per row group (K = I) or for the dense shared expert.
+template <typename T>
+__global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
+                                                  const T* const* wd_tab, const T* wd_one, int I,
+                                                  int H, T* __restrict__ Y) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  int grp, row0, mv, n0;
+  if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
+  const T* wd = pick(wd_tab, wd_one, grp);
+  OpDesc<T> a[1] = {{A + (int64_t)row0 * I, I, mv, I}};
+  OpDesc<T> b[1] = {{wd + (int64_t)n0 * I, I, H - n0, I}};
+  f32x16 acc[1][C::TN][C::TM];
+  zero_acc<C, 1>(acc);
+  mainloop<C, T, false, false, 1, 1>(acc, a, b, I, smem);
+  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv || n0 + n >= H) return;
+    store4(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+  });
+}
+
+// ------------------------------------------------------------------ combine
+// out[t] = sum_j w[t, j] * Y[inv_perm[t, j]] (+ s * Ys[t]); one wave per token.
+template <typename T>
+__global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
+                                                     const int* __restrict__ inv_perm,
+                                                     const float* __restrict__ w,
+                                                     const T* __restrict__ Ys, float s, int Tn,
+                                                     int k, int H, T* __restrict__ out) {
+  constexpr int V = Vec16<T>::N;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t TK = (int64_t)Tn * k;
+  int64_t pos[16];
+  float wj[16];
+  for (int j = 0; j < k; ++j) {
+    int64_t p = inv_perm[(int64_t)t * k + j];
+    pos[j] = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+    wj[j] = w[(int64_t)t * k + j];
+  }
+  for (int c = lane; c < H / V; c += 64) {
+    float acc[V], y[V];
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+    for (int j = 0; j < k; ++j) {
+      unpack16(ld16(Y + pos[j] * H + c * V), y, T());
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += wj[j] * y[i];
+    }
+    if (Ys) {
+      unpack16(ld16(Ys + (int64_t)t * H + c * V), y, T());
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += s * y[i];
+    }
+    st16(out + (int64_t)t * H + c * V, pack16(acc, T()));
+  }
+}
+
+// dw[t, j] = <dout[t], Y[pos]>,  dY[pos] = w[t, j] * dout[t].
+template <typename T>
+__global__ __launch_bounds__(256) void k_combine_bwd(const T* __restrict__ dout,
+                                                     const T* __restrict__ Y,
+                                                     const int* __restrict__ inv_perm,
+                                                     const float* __restrict__ w, int Tn, int k,
+                                                     int H, float* __restrict__ dw,
+                                                     T* __restrict__ dY) {
+  constexpr int V = Vec16<T>::N;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const int lane = threadIdx.x & 63;
+  const int64_t TK = (int64_t)Tn * k;
+  int64_t pos[16];
+  float wj[16], dot[16];
+  for (int j = 0; j < k; ++j) {
+    int64_t p = inv_perm[(int64_t)t * k + j];
+    pos[j] = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+    wj[j] = w[(int64_t)t * k + j];
+    dot[j] = 0.0f;
+  }
+  for (int c = lane; c < H / V; c += 64) {
+    float d[V], y[V], o[V];
+    unpack16(ld16(dout + (int64_t)t * H + c * V), d, T());
+    for (int j = 0; j < k; ++j) {
+      unpack16(ld16(Y + pos[j] * H + c * V), y, T());
+      float s = 0.0f;
+#pragma unroll
+      for (int i = 0; i < V; ++i) {
+        s += d[i] * y[i];
+        o[i] = wj[j] * d[i];
+      }
+      dot[j] += s;
+      st16(dY + pos[j] * H + c * V, pack16(o, T()));
+    }
+  }
+  for (int j = 0; j < k; ++j) {
+    const float r = wave_sum(dot[j]);
+    if (lane == 0) dw[(int64_t)t * k + j] = r;
+  }
+}
+
+// ------------------------------------------------------------------ expert GEMMs (backward)
+// dA = alpha * dY Wd (NN, K = H), then the SwiGLU backward in the epilogue:
+// dG = dA * U * silu'(G), dU = dA * silu(G).
+template <typename T>
+__global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, RowGroups groups,
+                                                    const T* const* wd_tab, const T* wd_one,
+                                                    int H, int N, float alpha,
+                                                    const T* __restrict__ G,
+                                                    const T* __restrict__ U,
+                                                    T* __restrict__ dG, T* __restrict__ dU) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  int grp, row0, mv, n0;
+  if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
+  const T* wd = pick(wd_tab, wd_one, grp);  // [H, N]: element (n, k=h) at wd + h*N + n
+  OpDesc<T> a[1] = {{dY + (int64_t)row0 * H, H, mv, H}};
+  OpDesc<T> b[1] = {{wd + n0, N, N - n0, H}};
+  f32x16 acc[1][C::TN][C::TM];
+  zero_acc<C, 1>(acc);
+  mainloop<C, T, false, true, 1, 1>(acc, a, b, H, smem);
+  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv || n0 + n >= N) return;
+    const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
+    float g[4], u[4], dg[4], du[4];
+    load4(G + o, g);
+    load4(U + o, u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float da = alpha * v[0][i];
+      const float sg = sigmoid_f(g[i]);
+      dg[i] = da * u[i] * (sg * (1.0f + g[i] * (1.0f - sg)));
+      du[i] = da * (g[i] * sg);
+    }
+    store4(dG + o, dg);
+    store4(dU + o, du);
+  });
+}
+
+// dX = dG Wg + dU Wu (NN, K = I twice) per row group.
+template <typename T>
+__global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
+                                                      const T* __restrict__ dU, RowGroups groups,
+                                                      const T* const* wg_tab, const T* wg_one,
+                                                      const T* const* wu_tab, const T* wu_one,
+                                                      int I, int H, T* __restrict__ dX) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  int grp, row0, mv, n0;
+  if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
+  const T* wg = pick(wg_tab, wg_one, grp);  // [I, H]: element (n=h, k=i) at wg + i*H + h
+  const T* wu = pick(wu_tab, wu_one, grp);
+  f32x16 acc[1][C::TN][C::TM];
+  zero_acc<C, 1>(acc);
+  {
+    OpDesc<T> a[1] = {{dG + (int64_t)row0 * I, I, mv, I}};
+    OpDesc<T> b[1] = {{wg + n0, H, H - n0, I}};
+    mainloop<C, T, false, true, 1, 1>(acc, a, b, I, smem);
+  }
+  __syncthreads();
+  {
+    OpDesc<T> a[1] = {{dU + (int64_t)row0 * I, I, mv, I}};
+    OpDesc<T> b[1] = {{wu + n0, H, H - n0, I}};
+    mainloop<C, T, false, true, 1, 1>(acc, a, b, I, smem);
+  }
+  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv || n0 + n >= H) return;
+    store4(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+  });
+}
+
+// Weight gradients, K-grouped over token rows (TN):
+//   W_a[g][m, n] = alpha * sum_r P_a[r, m] * Q[r, n],  r over the group's rows,
+// with NA = 1 (single) or 2 (two P operands sharing Q).  P is [rows, M]
+// (ld = ldp), Q is [rows, N] (ld = ldq), outputs [M, N].
+template <typename T, int NA>
+__global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
+                                               int64_t ldp, const T* __restrict__ Q, int64_t ldq,
+                                               KGroups groups, int M, int N, float alpha,
+                                               T* const* out0_tab, T* out0_one,
+                                               T* const* out1_tab, T* out1_one) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, NA, 1>()];
+  int grp, krow0, K, m0, n0;
+  if (!resolve_k(groups, M, N, C::BM, C::BN, grp, krow0, K, m0, n0)) return;
+  OpDesc<T> a[NA];
+  a[0] = {P0 + krow0 * ldp + m0, ldp, M - m0, K};
+  if constexpr (NA == 2) a[1] = {P1 + krow0 * ldp + m0, ldp, M - m0, K};
+  OpDesc<T> b[1] = {{Q + krow0 * ldq + n0, ldq, N - n0, K}};
+  f32x16 acc[NA][C::TN][C::TM];
+  zero_acc<C, NA>(acc);
+  mainloop<C, T, true, true, NA, 1>(acc, a, b, K, smem);
+  T* o0 = pick(out0_tab, out0_one, grp);
+  T* o1 = NA == 2 ? pick(out1_tab, out1_one, grp) : nullptr;
+  const int mv = min(C::BM, M - m0);
+  for_each_frag<C, NA>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv || n0 + n >= N) return;
+    const int64_t o = (int64_t)(m0 + m) * N + n0 + n;
+    float r[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = alpha * v[0][i];
+    store4(o0 + o, r);
+    if constexpr (NA == 2) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] = alpha * v[1][i];
+      store4(o1 + o, r);
+    }
+  });
+}
+
+// ------------------------------------------------------------------ router backward
+// d logits from the routing-weight gradients dw, the aux loss (through P_e)
+// and the z loss, through the softmax Jacobian; one wave per token.
+template <typename T, int EPL>
+__global__ __launch_bounds__(256) void k_router_bwd(
+    const float* __restrict__ probs, const float* __restrict__ lse, const int* __restrict__ idx,
+    const float* __restrict__ w, const float* __restrict__ dw, const float* __restrict__ P,
+    const int* __restrict__ counts, const float* __restrict__ d_aux,
+    const float* __restrict__ d_z, int Tn, int E, int Epad, int k, float tau, int norm,
+    float c_sw, float c_sq, float* __restrict__ dlogits, T* __restrict__ dlogits_t) {
+  const int lane = threadIdx.x & 63;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const float daux = d_aux ? *d_aux : 0.0f;
+  const float dz = d_z ? *d_z : 0.0f;
+  const float inv_tk = 1.0f / ((float)Tn * (float)k);
+  float p[EPL], dp[EPL];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    p[i] = e < E ? probs[(int64_t)t * E + e] : 0.0f;
+    dp[i] = e < E ? daux * (float)E *
+                        (c_sw * ((float)counts[e] * inv_tk) + 2.0f * c_sq * P[e]) / (float)Tn
+                  : 0.0f;
+  }
+  float psum = 0.0f, wdot = 0.0f;
+  if (norm) {
+    for (int j = 0; j < k; ++j) {
+      psum += probs[(int64_t)t * E + idx[(int64_t)t * k + j]];
+      wdot += dw[(int64_t)t * k + j] * w[(int64_t)t * k + j];
+    }
+  }
+  for (int j = 0; j < k; ++j) {
+    const int e = idx[(int64_t)t * k + j];
+    const float g = norm ? (dw[(int64_t)t * k + j] - wdot) / psum : dw[(int64_t)t * k + j];
+#pragma unroll
+    for (int i = 0; i < EPL; ++i)
+      if (lane + 64 * i == e) dp[i] += g;
+  }
+  float dot = 0.0f;
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) dot += p[i] * dp[i];
+  dot = wave_sum(dot);
+  const float zc = dz * 2.0f / (float)Tn * lse[t];
+#pragma unroll
+  for (int i = 0; i < EPL; ++i) {
+    const int e = lane + 64 * i;
+    if (e < E) {
+      const float ds = p[i] * (dp[i] - dot) + zc * p[i];
+      const float dl = ds / tau;
+      dlogits[(int64_t)t * E + e] = dl;
+      dlogits_t[(int64_t)t * Epad + e] = from_f<T>(dl);
+    } else if (e < Epad) {
+      dlogits_t[(int64_t)t * Epad + e] = from_f<T>(0.0f);
+    }
+  }
+}
+
+// dx = dlogits Wr (NN, K = E) + sum_j dXp[inv_perm[t, j]] + dxs[t].
+template <typename T>
+__global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, int Epad, int E,
+                                                      const T* __restrict__ wr, int Tn, int H,
+                                                      const T* __restrict__ dXp,
+                                                      const int* __restrict__ inv_perm, int k,
+                                                      const T* __restrict__ dxs,
+                                                      T* __restrict__ dx) {
+  using C = typename GemmTiling<T>::C;
+  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  RowGroups g{nullptr, nullptr, 1, Tn};
+  int grp, row0, mv, n0;
+  if (!resolve_rows(g, H, C::BM, C::BN, grp, row0, mv, n0)) return;
+  OpDesc<T> a[1] = {{dl + (int64_t)row0 * Epad, Epad, mv, Epad}};
+  OpDesc<T> b[1] = {{wr + n0, H, H - n0, E}};
+  f32x16 acc[1][C::TN][C::TM];
+  zero_acc<C, 1>(acc);
+  mainloop<C, T, false, true, 1, 1>(acc, a, b, Epad, smem);
+  const int64_t TK = (int64_t)Tn * k;
+  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv || n0 + n >= H) return;
+    const int t = row0 + m;
+    float r[4], q[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r[i] = v[0][i];
+    for (int j = 0; j < k; ++j) {
+      int64_t p = inv_perm[(int64_t)t * k + j];
+      p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+      load4(dXp + p * H + n0 + n, q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] += q[i];
+    }
+    if (dxs) {
+      load4(dxs + (int64_t)t * H + n0 + n, q);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r[i] += q[i];
+    }
+    store4(dx + (int64_t)t * H + n0 + n, r);
+  });
+}
+
+__global__ void k_has_grad(const int* __restrict__ counts, int E, uint8_t* __restrict__ has_grad) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e < E) has_grad[e] = counts[e] > 0 ? 1 : 0;
+}
+
+}  // namespace moe

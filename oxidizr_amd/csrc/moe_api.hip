@@ -1,0 +1,774 @@
+// C ABI of the MoE layer: plan, buffer layouts and the forward / backward
+// launch sequences.  Declared in include/moe_hip.h.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+#include <vector>
+
+#include "../../include/moe_hip.h"
+#include "kernels.hpp"
+
+using namespace moe;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+moe_status fail(moe_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+#define HIP_TRY(expr)                                                                   \
+  do {                                                                                  \
+    hipError_t _e = (expr);                                                             \
+    if (_e != hipSuccess)                                                               \
+      return fail(_e == hipErrorOutOfMemory ? MOE_ERR_OOM : MOE_ERR_HIP, "%s: %s (%s:%d)", \
+                  #expr, hipGetErrorString(_e), __FILE__, __LINE__);                    \
+  } while (0)
+
+#define LAUNCH_CHECK()                                                                   \
+  do {                                                                                   \
+    hipError_t _e = hipGetLastError();                                                   \
+    if (_e != hipSuccess)                                                                \
+      return fail(MOE_ERR_HIP, "kernel launch: %s (%s:%d)", hipGetErrorString(_e), __FILE__, \
+                  __LINE__);                                                             \
+  } while (0)
+
+constexpr size_t kAlign = 256;
+size_t align_up(size_t v) { return (v + kAlign - 1) / kAlign * kAlign; }
+
+// Bump allocator over a caller buffer: records offsets of named regions.
+struct Carve {
+  size_t off = 0;
+  size_t take(size_t bytes) {
+    size_t o = off;
+    off = align_up(off + bytes);
+    return o;
+  }
+};
+
+struct SavedLayout {
+  size_t f[MOE_SAVED_NUM_FIELDS];
+  size_t fbytes[MOE_SAVED_NUM_FIELDS];
+  size_t tile_prefix, sG, sU, sA;
+  size_t total;
+};
+
+struct WsLayout {
+  // forward
+  size_t block_hist, block_base, colpart, sY;
+  // backward
+  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs;
+  size_t total;
+};
+
+int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
+int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
+int round8(int v) { return (v + 7) / 8 * 8; }
+
+}  // namespace
+
+struct moe_plan {
+  moe_config cfg;
+  int device;
+  // device pointer tables: 0 gate, 1 up, 2 down (weights); 3..5 their grads
+  void** d_tab = nullptr;
+  void** h_tab = nullptr;       // pinned host staging
+  std::vector<const void*> cached[6];
+  bool profiling = false;
+  struct Pending { int stage; hipEvent_t a, b; };
+  std::vector<Pending> pending;
+  std::vector<hipEvent_t> free_events;
+  float stage_ms[MOE_NUM_STAGES] = {};
+  int32_t stage_calls[MOE_NUM_STAGES] = {};
+
+  int E() const { return cfg.num_experts; }
+  int es() const { return elt_size(cfg.dtype); }
+
+  SavedLayout saved_layout(int64_t T) const {
+    const int E = cfg.num_experts, k = cfg.experts_per_tok, H = cfg.hidden,
+              I = cfg.intermediate, S = cfg.shared_intermediate;
+    const int64_t TK = T * k;
+    const size_t b = es();
+    SavedLayout L{};
+    Carve c;
+    auto fld = [&](int id, size_t bytes) { L.f[id] = c.take(bytes); L.fbytes[id] = bytes; };
+    fld(MOE_SAVED_LOGITS, 4 * T * E);
+    fld(MOE_SAVED_PROBS, 4 * T * E);
+    fld(MOE_SAVED_LSE, 4 * T);
+    fld(MOE_SAVED_TOPK_IDX, 4 * TK);
+    fld(MOE_SAVED_TOPK_W, 4 * TK);
+    fld(MOE_SAVED_COUNTS, 4 * (size_t)E);
+    fld(MOE_SAVED_OFFSETS, 4 * (size_t)(E + 1));
+    fld(MOE_SAVED_PERM, 4 * TK);
+    fld(MOE_SAVED_INV_PERM, 4 * TK);
+    fld(MOE_SAVED_MEAN_PROB, 4 * (size_t)E);
+    L.tile_prefix = c.take(4 * (size_t)kNumTileBM * (E + 1));
+    fld(MOE_SAVED_X_PERM, b * TK * H);
+    fld(MOE_SAVED_GATE_ACT, b * TK * I);
+    fld(MOE_SAVED_UP_ACT, b * TK * I);
+    fld(MOE_SAVED_SWIGLU, b * TK * I);
+    fld(MOE_SAVED_EXPERT_OUT, b * TK * H);
+    L.sG = c.take(b * T * S);
+    L.sU = c.take(b * T * S);
+    L.sA = c.take(b * T * S);
+    L.total = c.off;
+    return L;
+  }
+
+  WsLayout ws_layout(int64_t T) const {
+    const int E = cfg.num_experts, k = cfg.experts_per_tok, H = cfg.hidden,
+              I = cfg.intermediate, S = cfg.shared_intermediate;
+    const int64_t TK = T * k;
+    const size_t b = es();
+    const int nb = ceil_div(T, 256), nrb = ceil_div(T, 64);
+    WsLayout L{};
+    Carve f;
+    L.block_hist = f.take(4 * (size_t)nb * E);
+    L.block_base = f.take(4 * (size_t)nb * E);
+    L.colpart = f.take(4 * (size_t)nrb * E);
+    L.sY = f.take(b * T * H);
+    Carve g;
+    g.take(4 * (size_t)nrb * E);  // column partials of the router-bias gradient (offset 0)
+    L.dw = g.take(4 * TK);
+    L.dY = g.take(b * TK * H);
+    L.dG = g.take(b * TK * I);
+    L.dU = g.take(b * TK * I);
+    L.dXp = g.take(b * TK * H);
+    L.dlogits = g.take(4 * T * E);
+    L.dlogits_t = g.take(b * T * round8(E));
+    L.sdG = g.take(b * T * S);
+    L.sdU = g.take(b * T * S);
+    L.dxs = g.take(b * T * H);
+    L.total = f.off > g.off ? f.off : g.off;
+    return L;
+  }
+
+  hipEvent_t event() {
+    if (!free_events.empty()) {
+      hipEvent_t e = free_events.back();
+      free_events.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+};
+
+namespace {
+
+// Records events around one stage when profiling is on.
+struct StageTimer {
+  moe_plan* p;
+  hipStream_t s;
+  int stage;
+  hipEvent_t a = nullptr;
+  StageTimer(moe_plan* p_, hipStream_t s_, int st) : p(p_), s(s_), stage(st) {
+    if (p->profiling) {
+      a = p->event();
+      if (a) (void)hipEventRecord(a, s);
+    }
+  }
+  ~StageTimer() {
+    if (a) {
+      hipEvent_t b = p->event();
+      if (b) {
+        (void)hipEventRecord(b, s);
+        p->pending.push_back({stage, a, b});
+      } else {
+        p->free_events.push_back(a);
+      }
+    }
+  }
+};
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+moe_status upload_tables(moe_plan* p, hipStream_t s, int first, const void* const* tabs[3]) {
+  const int E = p->E();
+  bool changed = false;
+  for (int i = 0; i < 3; ++i) {
+    if (!tabs[i]) continue;
+    auto& c = p->cached[first + i];
+    if (c.size() != (size_t)E || memcmp(c.data(), tabs[i], sizeof(void*) * E) != 0) changed = true;
+  }
+  if (!changed) return MOE_OK;
+  // the staging buffer may still feed an earlier copy on this stream
+  HIP_TRY(hipStreamSynchronize(s));
+  for (int i = 0; i < 3; ++i) {
+    if (!tabs[i]) continue;
+    for (int e = 0; e < E; ++e) {
+      if (!tabs[i][e] || !aligned16(tabs[i][e]))
+        return fail(MOE_ERR_INVALID, "expert %d pointer %d is NULL or not 16-byte aligned", e, i);
+    }
+    memcpy(p->h_tab + (size_t)(first + i) * E, tabs[i], sizeof(void*) * E);
+    p->cached[first + i].assign(tabs[i], tabs[i] + E);
+  }
+  HIP_TRY(hipMemcpyAsync(p->d_tab + (size_t)first * E, p->h_tab + (size_t)first * E,
+                         sizeof(void*) * 3 * E, hipMemcpyHostToDevice, s));
+  return MOE_OK;
+}
+
+int route_epl(int E) { return E <= 64 ? 1 : E <= 128 ? 2 : E <= 256 ? 4 : E <= 512 ? 8 : 16; }
+
+template <int EPL>
+void launch_route(hipStream_t s, int grid, const float* logits, int T, int E, int k, float tau,
+                  int norm, float* probs, float* lse, int* idx, float* w) {
+  hipLaunchKernelGGL((k_route<EPL>), dim3(grid), dim3(256), 0, s, logits, T, E, k, tau, norm,
+                     probs, lse, idx, w);
+}
+
+// Routing (from logits already in saved), losses' P statistics and dispatch.
+template <typename D>
+moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
+                       const SavedLayout& L, const WsLayout& W) {
+  const moe_config& c = p->cfg;
+  const int T = (int)T64, E = c.num_experts, k = c.experts_per_tok;
+  float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
+  float* probs = (float*)(saved + L.f[MOE_SAVED_PROBS]);
+  float* lse = (float*)(saved + L.f[MOE_SAVED_LSE]);
+  int* idx = (int*)(saved + L.f[MOE_SAVED_TOPK_IDX]);
+  float* w = (float*)(saved + L.f[MOE_SAVED_TOPK_W]);
+  int* counts = (int*)(saved + L.f[MOE_SAVED_COUNTS]);
+  int* offsets = (int*)(saved + L.f[MOE_SAVED_OFFSETS]);
+  int* perm = (int*)(saved + L.f[MOE_SAVED_PERM]);
+  int* inv = (int*)(saved + L.f[MOE_SAVED_INV_PERM]);
+  float* P = (float*)(saved + L.f[MOE_SAVED_MEAN_PROB]);
+  int* tprefix = (int*)(saved + L.tile_prefix);
+  {
+    StageTimer st(p, s, MOE_STAGE_ROUTE);
+    const int grid = ceil_div(T, 4);
+    const float tau = c.router_temperature;
+    switch (route_epl(E)) {
+      case 1: launch_route<1>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
+      case 2: launch_route<2>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
+      case 4: launch_route<4>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
+      case 8: launch_route<8>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
+      default: launch_route<16>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
+    }
+    LAUNCH_CHECK();
+    const int nrb = ceil_div(T, 64);
+    float* part = (float*)(ws + W.colpart);
+    hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, probs, T,
+                       E, part);
+    hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, s, part, nrb, E,
+                       1.0f / (float)T, P);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_DISPATCH);
+    const int nb = ceil_div(T, 256);
+    int* bh = (int*)(ws + W.block_hist);
+    int* bb = (int*)(ws + W.block_base);
+    hipLaunchKernelGGL(k_hist, dim3(nb), dim3(256), sizeof(int) * E, s, idx, T, k, E, bh);
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(256), 0, s, bh, nb, E, bb, counts, offsets, tprefix);
+    int nbits = 0;
+    while ((1 << nbits) <= E) ++nbits;
+    hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), sizeof(int) * 8 * E, s, idx, T, k, E,
+                       nbits, bb, perm, inv);
+    LAUNCH_CHECK();
+  }
+  return MOE_OK;
+}
+
+int tile_slot(int bm) {
+  switch (bm) {
+    case 16: return 0; case 32: return 1; case 64: return 2; case 128: return 3; default: return 4;
+  }
+}
+
+template <typename D>
+moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
+                        const moe_weights* w, D* out, float* aux, float* z, char* saved,
+                        char* ws) {
+  using C = typename GemmTiling<D>::C;
+  const moe_config& c = p->cfg;
+  const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
+            I = c.intermediate, S = c.shared_intermediate;
+  const int64_t TK = T64 * k;
+  const SavedLayout L = p->saved_layout(T64);
+  const WsLayout W = p->ws_layout(T64);
+  float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
+  {
+    StageTimer st(p, s, MOE_STAGE_ROUTER_GEMM);
+    const int grid = ceil_div(T, C::BM) * ceil_div(E, C::BN);
+    hipLaunchKernelGGL(k_router_logits<D>, dim3(grid), dim3(256), 0, s, x, (const D*)w->router,
+                       c.has_router_bias ? w->router_bias : nullptr, logits, T, H, E);
+    LAUNCH_CHECK();
+  }
+  moe_status r = run_routing<D>(p, s, T64, saved, ws, L, W);
+  if (r != MOE_OK) return r;
+  const int* counts = (const int*)(saved + L.f[MOE_SAVED_COUNTS]);
+  const int* offsets = (const int*)(saved + L.f[MOE_SAVED_OFFSETS]);
+  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(C::BM) * (E + 1);
+  const int* perm = (const int*)(saved + L.f[MOE_SAVED_PERM]);
+  const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
+  const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
+  D* xp = (D*)(saved + L.f[MOE_SAVED_X_PERM]);
+  D* G = (D*)(saved + L.f[MOE_SAVED_GATE_ACT]);
+  D* U = (D*)(saved + L.f[MOE_SAVED_UP_ACT]);
+  D* A = (D*)(saved + L.f[MOE_SAVED_SWIGLU]);
+  D* Y = (D*)(saved + L.f[MOE_SAVED_EXPERT_OUT]);
+  {
+    StageTimer st(p, s, MOE_STAGE_GATHER);
+    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(TK, 4)), dim3(256), 0, s, x, perm, T, k, H, xp);
+    LAUNCH_CHECK();
+  }
+  const D* const* tg = (const D* const*)p->d_tab;
+  const D* const* tu = (const D* const*)(p->d_tab + E);
+  const D* const* td = (const D* const*)(p->d_tab + 2 * E);
+  const RowGroups rg{offsets, tprefix, E, 0};
+  const int mtiles_max = ceil_div(TK, C::BM) + E;
+  {
+    StageTimer st(p, s, MOE_STAGE_GATEUP_FWD);
+    const int grid = mtiles_max * ceil_div(I, C::BN);
+    hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr, tu,
+                       nullptr, H, I, G, U, A);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_DOWN_FWD);
+    const int grid = mtiles_max * ceil_div(H, C::BN);
+    hipLaunchKernelGGL(k_down_fwd<D>, dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I, H, Y);
+    LAUNCH_CHECK();
+  }
+  D* sY = nullptr;
+  if (S > 0) {
+    StageTimer st(p, s, MOE_STAGE_SHARED_FWD);
+    D* sG = (D*)(saved + L.sG);
+    D* sU = (D*)(saved + L.sU);
+    D* sA = (D*)(saved + L.sA);
+    sY = (D*)(ws + W.sY);
+    const RowGroups dense{nullptr, nullptr, 1, T};
+    hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(ceil_div(T, C::BM) * ceil_div(S, C::BN)), dim3(256),
+                       0, s, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                       (const D*)w->shared_up, H, S, sG, sU, sA);
+    hipLaunchKernelGGL(k_down_fwd<D>, dim3(ceil_div(T, C::BM) * ceil_div(H, C::BN)), dim3(256), 0,
+                       s, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_COMBINE_FWD);
+    hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, Y, inv, topw,
+                       sY, c.shared_expert_scale, T, k, H, out);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_LOSSES);
+    hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, s,
+                       (const float*)(saved + L.f[MOE_SAVED_MEAN_PROB]), counts,
+                       (const float*)(saved + L.f[MOE_SAVED_LSE]), T, E, k, c.aux_switch_coef,
+                       c.aux_sqprob_coef, aux, z);
+    LAUNCH_CHECK();
+  }
+  return MOE_OK;
+}
+
+template <int EPL, typename D>
+void launch_router_bwd(hipStream_t s, int grid, const float* probs, const float* lse,
+                       const int* idx, const float* w, const float* dw, const float* P,
+                       const int* counts, const float* d_aux, const float* d_z, int T, int E,
+                       int Epad, int k, const moe_config& c, float* dl, D* dlt) {
+  hipLaunchKernelGGL((k_router_bwd<D, EPL>), dim3(grid), dim3(256), 0, s, probs, lse, idx, w, dw,
+                     P, counts, d_aux, d_z, T, E, Epad, k, c.router_temperature,
+                     c.norm_topk_prob, c.aux_switch_coef, c.aux_sqprob_coef, dl, dlt);
+}
+
+template <typename D>
+moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
+                         const float* d_aux, const float* d_z, const D* x, const moe_weights* w,
+                         const char* saved, char* ws, D* dx, const moe_grads* g,
+                         uint8_t* has_grad) {
+  using C = typename GemmTiling<D>::C;
+  const moe_config& c = p->cfg;
+  const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
+            I = c.intermediate, S = c.shared_intermediate;
+  const int Epad = round8(E);
+  const int64_t TK = T64 * k;
+  const SavedLayout L = p->saved_layout(T64);
+  const WsLayout W = p->ws_layout(T64);
+  const int* counts = (const int*)(saved + L.f[MOE_SAVED_COUNTS]);
+  const int* offsets = (const int*)(saved + L.f[MOE_SAVED_OFFSETS]);
+  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(C::BM) * (E + 1);
+  const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
+  const int* idx = (const int*)(saved + L.f[MOE_SAVED_TOPK_IDX]);
+  const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
+  const float* probs = (const float*)(saved + L.f[MOE_SAVED_PROBS]);
+  const float* lse = (const float*)(saved + L.f[MOE_SAVED_LSE]);
+  const float* P = (const float*)(saved + L.f[MOE_SAVED_MEAN_PROB]);
+  const D* xp = (const D*)(saved + L.f[MOE_SAVED_X_PERM]);
+  const D* G = (const D*)(saved + L.f[MOE_SAVED_GATE_ACT]);
+  const D* U = (const D*)(saved + L.f[MOE_SAVED_UP_ACT]);
+  const D* A = (const D*)(saved + L.f[MOE_SAVED_SWIGLU]);
+  const D* Y = (const D*)(saved + L.f[MOE_SAVED_EXPERT_OUT]);
+  float* dw = (float*)(ws + W.dw);
+  D* dY = (D*)(ws + W.dY);
+  D* dG = (D*)(ws + W.dG);
+  D* dU = (D*)(ws + W.dU);
+  D* dXp = (D*)(ws + W.dXp);
+  float* dl = (float*)(ws + W.dlogits);
+  D* dlt = (D*)(ws + W.dlogits_t);
+  const D* const* tg = (const D* const*)p->d_tab;
+  const D* const* tu = (const D* const*)(p->d_tab + E);
+  const D* const* td = (const D* const*)(p->d_tab + 2 * E);
+  D* const* tdg = (D* const*)(p->d_tab + 3 * E);
+  D* const* tdu = (D* const*)(p->d_tab + 4 * E);
+  D* const* tdd = (D* const*)(p->d_tab + 5 * E);
+  const RowGroups rg{offsets, tprefix, E, 0};
+  const KGroups kg{offsets, E, 0};
+  const int mtiles_max = ceil_div(TK, C::BM) + E;
+  {
+    StageTimer st(p, s, MOE_STAGE_COMBINE_BWD);
+    hipLaunchKernelGGL(k_combine_bwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, dout, Y, inv,
+                       topw, T, k, H, dw, dY);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_DOWN_DGRAD);
+    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(mtiles_max * ceil_div(I, C::BN)), dim3(256), 0, s,
+                       dY, rg, td, nullptr, H, I, 1.0f, G, U, dG, dU);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_DOWN_WGRAD);
+    const int grid = E * ceil_div(H, C::BM) * ceil_div(I, C::BN);
+    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
+                       (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_GATEUP_DGRAD);
+    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(mtiles_max * ceil_div(H, C::BN)), dim3(256), 0, s,
+                       dG, dU, rg, tg, nullptr, tu, nullptr, I, H, dXp);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_GATEUP_WGRAD);
+    const int grid = E * ceil_div(I, C::BM) * ceil_div(H, C::BN);
+    hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
+                       (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr);
+    LAUNCH_CHECK();
+  }
+  D* dxs = nullptr;
+  if (S > 0) {
+    StageTimer st(p, s, MOE_STAGE_SHARED_BWD);
+    const D* sG = (const D*)(saved + L.sG);
+    const D* sU = (const D*)(saved + L.sU);
+    const D* sA = (const D*)(saved + L.sA);
+    D* sdG = (D*)(ws + W.sdG);
+    D* sdU = (D*)(ws + W.sdU);
+    dxs = (D*)(ws + W.dxs);
+    const float sc = c.shared_expert_scale;
+    const RowGroups dense{nullptr, nullptr, 1, T};
+    const KGroups kdense{nullptr, 1, T};
+    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(ceil_div(T, C::BM) * ceil_div(S, C::BN)), dim3(256),
+                       0, s, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
+                       sdG, sdU);
+    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(H, C::BM) * ceil_div(S, C::BN)), dim3(256),
+                       0, s, dout, nullptr, (int64_t)H, sA, (int64_t)S, kdense, H, S, sc, nullptr,
+                       (D*)g->shared_down, nullptr, nullptr);
+    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(ceil_div(T, C::BM) * ceil_div(H, C::BN)), dim3(256),
+                       0, s, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                       (const D*)w->shared_up, S, H, dxs);
+    hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(ceil_div(S, C::BM) * ceil_div(H, C::BN)), dim3(256),
+                       0, s, sdG, sdU, (int64_t)S, x, (int64_t)H, kdense, S, H, 1.0f, nullptr,
+                       (D*)g->shared_gate, nullptr, (D*)g->shared_up);
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_ROUTER_BWD);
+    const int grid = ceil_div(T, 4);
+    switch (route_epl(E)) {
+      case 1: launch_router_bwd<1, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 2: launch_router_bwd<2, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 4: launch_router_bwd<4, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 8: launch_router_bwd<8, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      default: launch_router_bwd<16, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+    }
+    LAUNCH_CHECK();
+    const KGroups kdense{nullptr, 1, T};
+    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(E, C::BM) * ceil_div(H, C::BN)), dim3(256),
+                       0, s, dlt, nullptr, (int64_t)Epad, x, (int64_t)H, kdense, E, H, 1.0f,
+                       nullptr, (D*)g->router, nullptr, nullptr);
+    if (c.has_router_bias && g->router_bias) {
+      const int nrb = ceil_div(T, 64);
+      float* part = (float*)(ws);  // column partials at workspace offset 0
+      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, dl, T, E,
+                         part);
+      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, s, part, nrb, E,
+                         1.0f, g->router_bias);
+    }
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer st(p, s, MOE_STAGE_DX);
+    hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, C::BM) * ceil_div(H, C::BN)),
+                       dim3(256), 0, s, dlt, Epad, E, (const D*)w->router, T, H, dXp, inv, k, dxs,
+                       dx);
+    if (has_grad) hipLaunchKernelGGL(k_has_grad, dim3(ceil_div(E, 256)), dim3(256), 0, s, counts, E, has_grad);
+    LAUNCH_CHECK();
+  }
+  return MOE_OK;
+}
+
+moe_status check_plan(const moe_plan* p) {
+  if (!p) return fail(MOE_ERR_INVALID, "plan is NULL");
+  return MOE_OK;
+}
+
+moe_status validate_config(const moe_config* c) {
+  if (!c) return fail(MOE_ERR_INVALID, "config is NULL");
+  if (c->dtype != MOE_DTYPE_F32 && c->dtype != MOE_DTYPE_BF16)
+    return fail(MOE_ERR_INVALID, "dtype %d is not MOE_DTYPE_F32 or MOE_DTYPE_BF16", c->dtype);
+  if (c->hidden <= 0 || c->hidden % 8)
+    return fail(MOE_ERR_INVALID, "hidden (%d) must be a positive multiple of 8", c->hidden);
+  if (c->intermediate <= 0)
+    return fail(MOE_ERR_INVALID, "MoE cfg.moe.intermediate_size must be non-zero");
+  if (c->intermediate % 8)
+    return fail(MOE_ERR_INVALID, "intermediate_size (%d) must be a multiple of 8", c->intermediate);
+  if (c->shared_intermediate < 0 || c->shared_intermediate % 8)
+    return fail(MOE_ERR_INVALID, "shared_intermediate (%d) must be 0 or a multiple of 8",
+                c->shared_intermediate);
+  if (c->num_experts < 1 || c->num_experts > 1024)
+    return fail(MOE_ERR_INVALID, "num_experts (%d) must be in 1..1024", c->num_experts);
+  if (c->experts_per_tok < 1)
+    return fail(MOE_ERR_INVALID, "experts_per_tok (%d) must be at least 1", c->experts_per_tok);
+  if (c->experts_per_tok > c->num_experts)
+    return fail(MOE_ERR_INVALID, "MoE experts_per_tok (%d) must not exceed num_experts (%d)",
+                c->experts_per_tok, c->num_experts);
+  if (c->experts_per_tok > 16)
+    return fail(MOE_ERR_UNSUPPORTED, "experts_per_tok (%d) above 16 is not supported",
+                c->experts_per_tok);
+  if (!(c->router_temperature > 0.0f))
+    return fail(MOE_ERR_INVALID, "router_temperature must be positive");
+  return MOE_OK;
+}
+
+moe_status check_tokens(int64_t T) {
+  if (T < 0) return fail(MOE_ERR_INVALID, "num_tokens (%lld) is negative", (long long)T);
+  if (T > (1 << 24)) return fail(MOE_ERR_UNSUPPORTED, "num_tokens (%lld) above 2^24", (long long)T);
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+void moe_config_default(moe_config* cfg, int32_t hidden, int32_t num_experts,
+                        int32_t experts_per_tok, int32_t intermediate,
+                        int32_t shared_intermediate) {
+  if (!cfg) return;
+  memset(cfg, 0, sizeof(*cfg));
+  cfg->hidden = hidden;
+  cfg->num_experts = num_experts;
+  cfg->experts_per_tok = experts_per_tok;
+  cfg->intermediate = intermediate;
+  cfg->shared_intermediate = shared_intermediate;
+  cfg->dtype = MOE_DTYPE_BF16;
+  cfg->router_temperature = 1.0f;
+  cfg->shared_expert_scale = 1.0f;
+  cfg->aux_switch_coef = 1.0f;
+  cfg->aux_sqprob_coef = 1.0f;
+}
+
+moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
+  if (!out) return fail(MOE_ERR_INVALID, "plan output pointer is NULL");
+  *out = nullptr;
+  moe_status st = validate_config(cfg);
+  if (st != MOE_OK) return st;
+  int n = 0;
+  HIP_TRY(hipGetDeviceCount(&n));
+  if (device < 0 || device >= n) return fail(MOE_ERR_INVALID, "device %d out of range (%d)", device, n);
+  HIP_TRY(hipSetDevice(device));
+  moe_plan* p = new (std::nothrow) moe_plan();
+  if (!p) return fail(MOE_ERR_OOM, "host allocation of the plan failed");
+  p->cfg = *cfg;
+  p->device = device;
+  const size_t tab_bytes = sizeof(void*) * 6 * (size_t)cfg->num_experts;
+  hipError_t e = hipMalloc((void**)&p->d_tab, tab_bytes);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&p->h_tab, tab_bytes, hipHostMallocDefault);
+  if (e == hipSuccess) e = hipMemset(p->d_tab, 0, tab_bytes);
+  if (e != hipSuccess) {
+    moe_plan_destroy(p);
+    return fail(e == hipErrorOutOfMemory ? MOE_ERR_OOM : MOE_ERR_HIP, "plan tables: %s",
+                hipGetErrorString(e));
+  }
+  *out = p;
+  return MOE_OK;
+}
+
+moe_status moe_plan_destroy(moe_plan* p) {
+  if (!p) return MOE_OK;
+  for (auto& q : p->pending) {
+    hipEventSynchronize(q.b);
+    hipEventDestroy(q.a);
+    hipEventDestroy(q.b);
+  }
+  for (auto e : p->free_events) hipEventDestroy(e);
+  if (p->d_tab) hipFree(p->d_tab);
+  if (p->h_tab) hipHostFree(p->h_tab);
+  delete p;
+  return MOE_OK;
+}
+
+size_t moe_saved_bytes(const moe_plan* p, int64_t T) {
+  if (!p || T < 0) return 0;
+  return p->saved_layout(T).total;
+}
+
+size_t moe_workspace_bytes(const moe_plan* p, int64_t T) {
+  if (!p || T < 0) return 0;
+  return p->ws_layout(T).total;
+}
+
+moe_status moe_saved_field_range(const moe_plan* p, int64_t T, int32_t field, size_t* offset,
+                                 size_t* bytes) {
+  if (!p) return fail(MOE_ERR_INVALID, "plan is NULL");
+  if (field < 0 || field >= MOE_SAVED_NUM_FIELDS)
+    return fail(MOE_ERR_INVALID, "unknown saved field %d", field);
+  const SavedLayout L = p->saved_layout(T);
+  if (offset) *offset = L.f[field];
+  if (bytes) *bytes = L.fbytes[field];
+  return MOE_OK;
+}
+
+moe_status moe_forward(moe_plan* p, void* stream, int64_t T, const void* x, const moe_weights* w,
+                       void* out, float* aux_loss, float* z_loss, void* saved, void* workspace) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  if ((st = check_tokens(T)) != MOE_OK) return st;
+  if (!w) return fail(MOE_ERR_INVALID, "weights struct is NULL");
+  const moe_config& c = p->cfg;
+  if (T > 0 && (!x || !out || !saved || !workspace || !w->router || !w->gate || !w->up || !w->down))
+    return fail(MOE_ERR_INVALID, "a required pointer is NULL");
+  if (c.has_router_bias && !w->router_bias)
+    return fail(MOE_ERR_INVALID, "has_router_bias is set but router_bias is NULL");
+  if (c.shared_intermediate > 0 && (!w->shared_gate || !w->shared_up || !w->shared_down))
+    return fail(MOE_ERR_INVALID, "shared expert enabled but its weights are NULL");
+  const void* ptrs[] = {x, out, saved, workspace, w->router, w->shared_gate, w->shared_up,
+                        w->shared_down};
+  for (const void* q : ptrs)
+    if (q && !aligned16(q)) return fail(MOE_ERR_INVALID, "device pointers must be 16-byte aligned");
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(hipSetDevice(p->device));
+  if (T == 0) {
+    if (aux_loss) HIP_TRY(hipMemsetAsync(aux_loss, 0, sizeof(float), s));
+    if (z_loss) HIP_TRY(hipMemsetAsync(z_loss, 0, sizeof(float), s));
+    return MOE_OK;
+  }
+  const void* const* tabs[3] = {w->gate, w->up, w->down};
+  if ((st = upload_tables(p, s, 0, tabs)) != MOE_OK) return st;
+  if (c.dtype == MOE_DTYPE_BF16)
+    return forward_impl<bf16_t>(p, s, T, (const bf16_t*)x, w, (bf16_t*)out, aux_loss, z_loss,
+                                (char*)saved, (char*)workspace);
+  return forward_impl<float>(p, s, T, (const float*)x, w, (float*)out, aux_loss, z_loss,
+                             (char*)saved, (char*)workspace);
+}
+
+moe_status moe_backward(moe_plan* p, void* stream, int64_t T, const void* d_out,
+                        const float* d_aux, const float* d_z, const void* x,
+                        const moe_weights* w, const void* saved, void* workspace, void* dx,
+                        const moe_grads* g, uint8_t* has_grad) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  if ((st = check_tokens(T)) != MOE_OK) return st;
+  if (!w || !g) return fail(MOE_ERR_INVALID, "weights or grads struct is NULL");
+  const moe_config& c = p->cfg;
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(hipSetDevice(p->device));
+  if (T == 0) return MOE_OK;  // nothing routed: no gradient is written
+  if (!d_out || !x || !saved || !workspace || !dx || !w->router || !w->gate || !w->up ||
+      !w->down || !g->router || !g->gate || !g->up || !g->down)
+    return fail(MOE_ERR_INVALID, "a required pointer is NULL");
+  if (c.shared_intermediate > 0 &&
+      (!w->shared_gate || !w->shared_up || !w->shared_down || !g->shared_gate || !g->shared_up ||
+       !g->shared_down))
+    return fail(MOE_ERR_INVALID, "shared expert enabled but its weights or grads are NULL");
+  const void* ptrs[] = {d_out, x, saved, workspace, dx, w->router, g->router, g->shared_gate,
+                        g->shared_up, g->shared_down};
+  for (const void* q : ptrs)
+    if (q && !aligned16(q)) return fail(MOE_ERR_INVALID, "device pointers must be 16-byte aligned");
+  const void* const* tabs[3] = {w->gate, w->up, w->down};
+  if ((st = upload_tables(p, s, 0, tabs)) != MOE_OK) return st;
+  const void* const* gtabs[3] = {(const void* const*)g->gate, (const void* const*)g->up,
+                                 (const void* const*)g->down};
+  if ((st = upload_tables(p, s, 3, gtabs)) != MOE_OK) return st;
+  if (c.dtype == MOE_DTYPE_BF16)
+    return backward_impl<bf16_t>(p, s, T, (const bf16_t*)d_out, d_aux, d_z, (const bf16_t*)x, w,
+                                 (const char*)saved, (char*)workspace, (bf16_t*)dx, g, has_grad);
+  return backward_impl<float>(p, s, T, (const float*)d_out, d_aux, d_z, (const float*)x, w,
+                              (const char*)saved, (char*)workspace, (float*)dx, g, has_grad);
+}
+
+moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const float* logits,
+                                 void* saved, void* workspace) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  if ((st = check_tokens(T)) != MOE_OK) return st;
+  if (T == 0) return MOE_OK;
+  if (!logits || !saved || !workspace) return fail(MOE_ERR_INVALID, "a required pointer is NULL");
+  hipStream_t s = (hipStream_t)stream;
+  HIP_TRY(hipSetDevice(p->device));
+  const SavedLayout L = p->saved_layout(T);
+  const WsLayout W = p->ws_layout(T);
+  char* sv = (char*)saved;
+  HIP_TRY(hipMemcpyAsync(sv + L.f[MOE_SAVED_LOGITS], logits,
+                         sizeof(float) * (size_t)T * p->cfg.num_experts, hipMemcpyDeviceToDevice,
+                         s));
+  if (p->cfg.dtype == MOE_DTYPE_BF16) return run_routing<bf16_t>(p, s, T, sv, (char*)workspace, L, W);
+  return run_routing<float>(p, s, T, sv, (char*)workspace, L, W);
+}
+
+const char* moe_stage_name(int32_t stage) {
+  static const char* names[MOE_NUM_STAGES] = {
+      "router_gemm", "route", "dispatch", "gather", "gateup_fwd", "down_fwd", "shared_fwd",
+      "combine_fwd", "losses", "combine_bwd", "down_dgrad", "down_wgrad", "gateup_dgrad",
+      "gateup_wgrad", "shared_bwd", "router_bwd", "dx"};
+  if (stage < 0 || stage >= MOE_NUM_STAGES) return "unknown";
+  return names[stage];
+}
+
+moe_status moe_plan_set_profiling(moe_plan* p, int32_t enable) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  p->profiling = enable != 0;
+  return MOE_OK;
+}
+
+moe_status moe_plan_stage_times(moe_plan* p, float* ms, int32_t* calls, int32_t reset) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  for (auto& q : p->pending) {
+    HIP_TRY(hipEventSynchronize(q.b));
+    float t = 0.0f;
+    HIP_TRY(hipEventElapsedTime(&t, q.a, q.b));
+    p->stage_ms[q.stage] += t;
+    p->stage_calls[q.stage] += 1;
+    p->free_events.push_back(q.a);
+    p->free_events.push_back(q.b);
+  }
+  p->pending.clear();
+  for (int i = 0; i < MOE_NUM_STAGES; ++i) {
+    if (ms) ms[i] = p->stage_ms[i];
+    if (calls) calls[i] = p->stage_calls[i];
+    if (reset) {
+      p->stage_ms[i] = 0.0f;
+      p->stage_calls[i] = 0;
+    }
+  }
+  return MOE_OK;
+}
+
+const char* moe_last_error(void) { return g_last_error.c_str(); }
+const char* moe_version(void) { return "oxidizr-amd moe 0.1 (gfx950)"; }
+
+}  // extern "C"

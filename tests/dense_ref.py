@@ -1,0 +1,55 @@
+"""Dense MoE restatement on torch (CPU, float64) -- test infrastructure only.
+
+It computes the same layer as the oracle by a different algorithm: every
+expert runs on every token and a dense [T, E] gate matrix (zero outside the
+top-k) mixes the results, with no histogram, permutation or gather. Top-k uses
+torch's stable sort on -logits, so equal logits keep the lower expert index
+first. Gradients come from torch autograd, independent of the oracle's
+hand-derived backward. Semantics follow src/model.rs:1284-1290 (SwiGLU),
+src/model.rs:1834-1885 (layer contract) and docs/architecture/moe.md:149-153
+(softmax then top-k) in the reference.
+"""
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+
+def dense_moe(p, cfg, need_grad=True, d_aux=0.0, d_z=0.0):
+    """p: dict of numpy inputs (see oxidizr_amd.synth.host_problem). Returns
+    (out, aux, z, grads or None, routing dict)."""
+    T, H, E, k, I, S = cfg.T, cfg.H, cfg.E, cfg.k, cfg.I, cfg.S
+    t = {n: torch.tensor(np.asarray(v, np.float64), requires_grad=need_grad and n != "dout")
+         for n, v in p.items()}
+    x = t["x"]
+    logits = x @ t["router"].T
+    if cfg.has_bias:
+        logits = logits + t["router_bias"]
+    s = logits / cfg.tau
+    probs = torch.softmax(s, dim=-1)
+    lse = torch.logsumexp(s, dim=-1)
+    order = torch.sort(-logits.detach(), dim=-1, stable=True).indices[:, :k]
+    wsel = probs.gather(1, order)
+    if cfg.norm_topk:
+        wsel = wsel / wsel.sum(dim=-1, keepdim=True)
+    gate_mat = torch.zeros(T, E, dtype=torch.float64).scatter(1, order, wsel)
+    out = torch.zeros(T, H, dtype=torch.float64)
+    for e in range(E):
+        y = F.linear(F.silu(F.linear(x, t["gate"][e])) * F.linear(x, t["up"][e]), t["down"][e])
+        out = out + gate_mat[:, e:e + 1] * y
+    if S:
+        ys = F.linear(F.silu(F.linear(x, t["shared_gate"])) * F.linear(x, t["shared_up"]),
+                      t["shared_down"])
+        out = out + cfg.shared_scale * ys
+    counts = torch.bincount(order.flatten(), minlength=E).to(torch.float64)
+    f = counts / (T * k)
+    P = probs.mean(dim=0)
+    aux = E * (cfg.aux_switch * (f * P).sum() + cfg.aux_sqprob * (P * P).sum())
+    z = (lse * lse).mean()
+    routing = {"idx": order.numpy().astype(np.int32), "counts": counts.numpy().astype(np.int32),
+               "probs": probs.detach().numpy(), "logits": logits.detach().numpy()}
+    grads = None
+    if need_grad:
+        L = (out * t["dout"]).sum() + d_aux * aux + d_z * z
+        L.backward()
+        grads = {n: v.grad.numpy() for n, v in t.items() if n != "dout" and v.grad is not None}
+    return out.detach().numpy(), aux.item(), z.item(), grads, routing

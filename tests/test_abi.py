@@ -1,0 +1,91 @@
+"""CPU checks of the drop-in boundary: the C-ABI library loads, exports every
+entry point include/moe_hip.h declares, its structs match the ctypes mirror,
+and the host-side config validation follows the reference's messages
+(src/model.rs:1927-1958, src/config_convert.rs:380-404). No GPU calls."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from oxidizr_amd import _lib
+from oxidizr_amd.moe import ModelError, MoeConfig
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "moe_hip.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(moe_[a-z_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.load()
+    names = _declared()
+    assert "moe_forward" in names and "moe_backward" in names
+    for n in names:
+        assert hasattr(L, n), f"{n} declared in moe_hip.h but not exported"
+    assert sorted(_lib.EXPORTED) == names
+
+
+def test_struct_layouts_match_header():
+    # moe_config: 8 int32 + 4 float; moe_weights / moe_grads: 8 pointers
+    assert ctypes.sizeof(_lib.MoeConfigC) == 48
+    assert ctypes.sizeof(_lib.MoeWeightsC) == 64
+    assert ctypes.sizeof(_lib.MoeGradsC) == 64
+
+
+def test_config_defaults_and_names():
+    L = _lib.load()
+    c = _lib.MoeConfigC()
+    L.moe_config_default(ctypes.byref(c), 2048, 16, 2, 1408, 2816)
+    assert (c.hidden, c.num_experts, c.experts_per_tok, c.intermediate, c.shared_intermediate) == \
+        (2048, 16, 2, 1408, 2816)
+    assert c.dtype == _lib.MOE_DTYPE_BF16
+    assert c.router_temperature == 1.0 and c.shared_expert_scale == 1.0
+    assert c.aux_switch_coef == 1.0 and c.aux_sqprob_coef == 1.0
+    assert c.norm_topk_prob == 0 and c.has_router_bias == 0
+    names = [L.moe_stage_name(i).decode() for i in range(_lib.NUM_STAGES)]
+    assert names[0] == "router_gemm" and names[-1] == "dx"
+    assert L.moe_stage_name(_lib.NUM_STAGES).decode() == "unknown"
+    assert b"gfx950" in L.moe_version()
+
+
+def test_null_plan_is_an_error_not_a_crash():
+    L = _lib.load()
+    assert L.moe_saved_bytes(None, 16) == 0
+    assert L.moe_plan_set_profiling(None, 1) == 1
+    assert b"NULL" in L.moe_last_error()
+    w = _lib.MoeWeightsC()
+    assert L.moe_forward(None, None, 4, None, ctypes.byref(w), None, None, None, None, None) == 1
+
+
+def test_invalid_config_rejected_before_any_device_call():
+    L = _lib.load()
+    c = _lib.MoeConfigC()
+    L.moe_config_default(ctypes.byref(c), 64, 4, 5, 32, 0)  # k > E
+    h = ctypes.c_void_p()
+    assert L.moe_plan_create(ctypes.byref(c), 0, ctypes.byref(h)) == 1
+    assert b"must not exceed num_experts" in L.moe_last_error()
+    L.moe_config_default(ctypes.byref(c), 64, 4, 2, 0, 0)
+    assert L.moe_plan_create(ctypes.byref(c), 0, ctypes.byref(h)) == 1
+    assert b"intermediate_size must be non-zero" in L.moe_last_error()
+    L.moe_config_default(ctypes.byref(c), 60, 4, 2, 32, 0)
+    assert L.moe_plan_create(ctypes.byref(c), 0, ctypes.byref(h)) == 1
+
+
+def test_required_moe_dims_messages():
+    with pytest.raises(ModelError, match="must not exceed num_experts"):
+        MoeConfig(64, 4, 5, 32).required_moe_dims()
+    with pytest.raises(ModelError, match="intermediate_size must be non-zero"):
+        MoeConfig(64, 4, 2, 0).required_moe_dims()
+    with pytest.raises(ModelError, match="requires cfg.moe.intermediate_size"):
+        MoeConfig(64, 4, 2, None).required_moe_dims()
+    with pytest.raises(ModelError, match="experts_per_tok is missing"):
+        MoeConfig(64, 4, None, 32).required_moe_dims()
+    assert MoeConfig(64, 4, 2, 32).required_moe_dims() == (4, 2, 32)
+    # shared_expert_enabled: None means true (src/config.rs:127-129)
+    assert MoeConfig(64, 4, 2, 32).shared_width() == 32
+    assert MoeConfig(64, 4, 2, 32, shared_expert_enabled=False).shared_width() == 0

@@ -1,0 +1,186 @@
+"""GPU parity of the HIP MoE layer against the CPU oracle, through the C ABI.
+
+Bars:
+  * routing: on identical fp32 logits, top-k indices, expert counts, offsets
+    and the dispatch permutation match the oracle bit-exactly;
+  * fp32: outputs and gradients within 1e-5 relative (L2) error;
+  * bf16: outputs and gradients within 1e-2 relative L2 error.
+The oracle routes from the GPU's own logits (logits_in), so both sides take
+the same routing decisions; the GPU logits themselves are compared with
+tolerance.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import moe_oracle as mo
+from oxidizr_amd.moe import MoeConfig, Plan
+from oxidizr_amd.synth import zipf_bias
+from tests.gpu_helpers import Case, gpu_run, oracle_run, rel
+
+pytestmark = pytest.mark.gpu
+
+GRAD_NAMES = ("dx", "router", "gate", "up", "down")
+
+
+def _routing_equal(g, o):
+    np.testing.assert_array_equal(g["topk_idx"], o["topk_idx"])
+    np.testing.assert_array_equal(g["counts"], o["counts"])
+    np.testing.assert_array_equal(g["offsets"], o["offsets"])
+    np.testing.assert_array_equal(g["perm"], o["perm"])
+    np.testing.assert_array_equal(g["inv_perm"], o["inv_perm"])
+
+
+def _check(case, g, o, tol, backward=True):
+    errs = {"out": rel(g["out"], o["out"]),
+            "logits": rel(g["logits"], case_logits_ref(case)),
+            "probs": rel(g["probs"], o["probs"]),
+            "topk_w": rel(g["topk_w"], o["topk_w"])}
+    errs["aux"] = abs(float(g["aux"]) - o["aux"]) / max(abs(o["aux"]), 1e-30)
+    errs["z"] = abs(float(g["z"]) - o["z"]) / max(abs(o["z"]), 1e-30)
+    if backward:
+        np.testing.assert_array_equal(g["has_grad"], o["has_grad"])
+        hg = o["has_grad"].astype(bool)
+        errs["dx"] = rel(g["dx"], o["x"])
+        errs["d_router"] = rel(g["router"], o["router"])
+        if case.bias is not None:
+            errs["d_router_bias"] = rel(g["router_bias"], o["router_bias"])
+        for n in ("gate", "up", "down"):
+            errs["d_" + n] = rel(g[n][hg], o[n][hg])
+            # experts with no routed token have no gradient entry: untouched buffers
+            assert np.isnan(g[n][~hg]).all(), n
+        if case.S:
+            for n in ("shared_gate", "shared_up", "shared_down"):
+                errs["d_" + n] = rel(g[n], o[n])
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"{case}: over tolerance {tol}: {bad} (all: {errs})"
+    return errs
+
+
+def case_logits_ref(case):
+    p = case.p
+    lg = p["x"].astype(np.float64) @ p["router"].astype(np.float64).T
+    if case.bias is not None:
+        lg = lg + p["router_bias"]
+    return lg
+
+
+# ---------------------------------------------------------------- routing
+
+@pytest.mark.parametrize("T,E,k", [(1, 4, 2), (257, 8, 2), (1000, 16, 2), (777, 64, 6),
+                                   (64, 128, 8), (300, 256, 8), (40, 5, 5), (129, 1000, 16)])
+def test_routing_bitexact_on_identical_logits(T, E, k):
+    rng = np.random.default_rng(T * 7 + E)
+    # small integers: many exact ties, which must go to the lower expert index
+    logits = rng.integers(-3, 4, size=(T, E)).astype(np.float32)
+    cfg = MoeConfig(hidden_size=8, num_experts=E, experts_per_tok=k, intermediate_size=8,
+                    shared_expert_enabled=False)
+    dev = torch.device("cuda:0")
+    plan = Plan(cfg, torch.bfloat16, dev)
+    saved = plan.route_from_logits(torch.tensor(logits, device=dev))
+    torch.cuda.synchronize()
+    oc = mo.make_cfg(T, 8, E, k, 8)
+    probs, lse, idx, w = mo.route(oc, logits.astype(np.float64))
+    counts, offsets, perm, inv = mo.dispatch(idx, E)
+    f = lambda n: plan.saved_field(saved, T, n).cpu().numpy()
+    np.testing.assert_array_equal(f("topk_idx"), idx)
+    np.testing.assert_array_equal(f("counts"), counts)
+    np.testing.assert_array_equal(f("offsets"), offsets)
+    np.testing.assert_array_equal(f("perm"), perm)
+    np.testing.assert_array_equal(f("inv_perm"), inv)
+    assert rel(f("probs"), probs) < 1e-6
+    assert rel(f("lse"), lse) < 1e-6
+    assert rel(f("topk_w"), w) < 1e-6
+
+
+# ---------------------------------------------------------------- fp32
+
+FP32_CASES = [
+    dict(T=96, H=64, E=8, k=2, I=48, S=32),
+    dict(T=100, H=72, E=5, k=3, I=40, S=24, bias=True, norm_topk=True, tau=1.5,
+         shared_scale=0.5, aux_switch=0.3, aux_sqprob=2.0),
+    dict(T=1024, H=384, E=8, k=2, I=1024, S=0),     # BASELINE config 1 (fp32, CPU-runnable)
+    dict(T=33, H=136, E=12, k=12, I=16, S=0),       # k == E: every expert selected
+]
+
+
+@pytest.mark.parametrize("spec", FP32_CASES)
+def test_fp32_forward_backward_parity(spec):
+    spec = dict(spec)
+    bias = zipf_bias(spec["E"], beta=0.5) if spec.pop("bias", False) else None
+    case = Case(**spec, dtype="f32", bias=bias)
+    g = gpu_run(case, d_aux=0.01, d_z=0.001)
+    o = oracle_run(case, g["logits"], d_aux=0.01, d_z=0.001)
+    _routing_equal(g, o)
+    _check(case, g, o, 1e-5)
+
+
+def test_fp32_unrouted_expert_keeps_no_gradient():
+    bias = np.array([0, 0, -1e4, 0, 0, -1e4], np.float32)  # experts 2 and 5 never chosen
+    case = Case(T=80, H=64, E=6, k=2, I=32, S=0, dtype="f32", bias=bias)
+    g = gpu_run(case, d_aux=0.1)
+    o = oracle_run(case, g["logits"], d_aux=0.1)
+    assert list(g["has_grad"]) == [1, 1, 0, 1, 1, 0]
+    _check(case, g, o, 1e-5)
+
+
+# ---------------------------------------------------------------- bf16
+
+BF16_CASES = [
+    # shapes of BASELINE configs 2, 3, 5 scaled down; skewed routing with empty experts
+    dict(T=512, H=256, E=16, k=2, I=176, S=352),
+    dict(T=384, H=128, E=64, k=6, I=64, S=128, skew=3.0),
+    dict(T=256, H=256, E=256, k=8, I=128, S=128),
+    dict(T=200, H=192, E=20, k=4, I=88, S=0, bias=True, norm_topk=True),
+]
+
+
+@pytest.mark.parametrize("spec", BF16_CASES)
+def test_bf16_forward_backward_parity(spec):
+    spec = dict(spec)
+    skew = spec.pop("skew", None)
+    bias = None
+    if skew is not None:
+        bias = zipf_bias(spec["E"], s=1.2, beta=skew)
+    elif spec.pop("bias", False):
+        bias = zipf_bias(spec["E"], beta=0.5)
+    case = Case(**spec, dtype="bf16", w_std=0.05, bias=bias)
+    g = gpu_run(case, d_aux=0.01, d_z=0.001)
+    o = oracle_run(case, g["logits"], d_aux=0.01, d_z=0.001)
+    _routing_equal(g, o)
+    if skew is not None:
+        assert (g["counts"] == 0).any(), "skewed case should leave some experts empty"
+    _check(case, g, o, 1e-2)
+
+
+def test_bf16_small_token_forward():
+    # BASELINE config 4 shape scaled in H and I: 64 tokens, 128 experts, top-8, no shared
+    case = Case(T=64, H=512, E=128, k=8, I=192, S=0, dtype="bf16", w_std=0.05)
+    g = gpu_run(case, backward=False)
+    o = oracle_run(case, g["logits"], backward=False)
+    _routing_equal(g, o)
+    _check(case, g, o, 1e-2, backward=False)
+
+
+# ---------------------------------------------------------------- reproducibility
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_bitwise_reproducible(dtype):
+    case = Case(T=300, H=128, E=16, k=4, I=64, S=64, dtype=dtype, w_std=0.05)
+    a = gpu_run(case, d_aux=0.01, d_z=0.001)
+    b = gpu_run(case, d_aux=0.01, d_z=0.001)
+    for n in ("out", "aux", "z", "dx", "router", "gate", "up", "down", "shared_down"):
+        np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_batch_invariance(dtype):
+    # Routing is per token (reference tests/data_parallel.rs:333-347), and no
+    # reduction crosses tokens in out or (with d_aux = d_z = 0) in dx: a token's
+    # rows are bitwise the same whether it is processed alone or in a batch.
+    case = Case(T=256, H=128, E=16, k=2, I=64, S=64, dtype=dtype, w_std=0.05, seed=3)
+    full = gpu_run(case)
+    sub = gpu_run(case, x=case.p["x"][:37], dout=case.p["dout"][:37])
+    np.testing.assert_array_equal(full["out"][:37], sub["out"])
+    np.testing.assert_array_equal(full["dx"][:37], sub["dx"])
+    np.testing.assert_array_equal(full["topk_idx"][:37], sub["topk_idx"])
