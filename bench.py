@@ -1,0 +1,266 @@
+#!/usr/bin/env python3
+"""MoE layer forward + backward throughput on one MI355X.
+
+One step = one forward and one backward pass of the MoE layer over one batch of
+synthetic tokens (every gradient written). Default workload
+(T=8192, H=2048, E=16, top-2, I=1408, shared 2816, bf16, alpha 0.01).
+Prints ONE JSON line. Other BASELINE configs: --config {1,3,4,5}.
+
+Inputs live in HBM before timing starts; random-init weights and N(0,1)
+activations/upstream gradients are generated on the device with a seeded
+generator. Configs 3 and 5 skew routing with a fixed per-expert logit bias.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def gen_weights(torch, shape, std, gen, dtype, dev):
+    t = torch.empty(shape, dtype=dtype, device=dev)
+    t.normal_(0.0, std, generator=gen)
+    return t
+
+
+def skew_bias(torch, wl, x, router, dev):
+    """Per-expert router logit bias that shapes the expert loads."""
+    import numpy as np
+    from oxidizr_amd.synth import lognormal_bias, zipf_bias
+    E, k = wl.E, wl.k
+    if wl.skew == "lognormal":
+        return torch.tensor(lognormal_bias(E, 0.5), device=dev), {}
+    if wl.skew != "zipf":
+        return None, {}
+    base = (x.float() @ router.float().t())
+    mean = wl.T * k / E
+
+    def counts(beta):
+        b = torch.tensor(zipf_bias(E, 1.2, beta), device=dev)
+        idx = torch.topk(base + b, k, dim=1).indices
+        return torch.bincount(idx.flatten(), minlength=E), b
+
+    lo, hi = 0.0, 20.0
+    for _ in range(30):  # busiest expert at ~8x the mean load
+        mid = 0.5 * (lo + hi)
+        c, _ = counts(mid)
+        if c.max().item() < 8 * mean:
+            lo = mid
+        else:
+            hi = mid
+    c, b = counts(lo)
+    b = b.clone()
+    if (c == 0).sum().item() == 0:  # push the tail: the least likely expert gets no token
+        b[int(np.argmin(b.cpu().numpy()))] = -1e4
+    return b, {"zipf_beta": round(lo, 4)}
+
+
+def cpu_baseline(wl, seconds, threads):
+    """The oracle (fp32, OpenMP) on a bounded sample of the same workload."""
+    import numpy as np
+    from oracle import moe_oracle as mo
+    mo.set_threads(threads)
+    E = wl.E if wl.E <= 16 else 16   # per-token cost depends on k, H, I, S, not E
+    k = min(wl.k, E)
+    rng = np.random.default_rng(1)
+
+    def normal(shape, std):
+        return (rng.standard_normal(shape, dtype=np.float32) * std)
+
+    W = {"router": normal((E, wl.H), wl.w_std), "gate": normal((E, wl.I, wl.H), wl.w_std),
+         "up": normal((E, wl.I, wl.H), wl.w_std), "down": normal((E, wl.H, wl.I), wl.w_std)}
+    if wl.S:
+        W.update(shared_gate=normal((wl.S, wl.H), wl.w_std), shared_up=normal((wl.S, wl.H), wl.w_std),
+                 shared_down=normal((wl.H, wl.S), wl.w_std))
+
+    grads = None
+
+    def run(T):
+        nonlocal grads
+        cfg = mo.make_cfg(T, wl.H, E, k, wl.I, wl.S)
+        o = mo.MoeOracle(cfg, 32)
+        x = normal((T, wl.H), 1.0)
+        dout = normal((T, wl.H), 1.0)
+        o.T = T
+        if grads is None:
+            grads = o.grad_buffers(0.0)   # weight-sized outputs, allocated outside the timing
+        grads["x"] = np.empty((T, wl.H), np.float32)
+        t0 = time.perf_counter()
+        o.forward(x, W["router"], W["gate"], W["up"], W["down"], None, W.get("shared_gate"),
+                  W.get("shared_up"), W.get("shared_down"))
+        if wl.backward:
+            o.backward(dout, d_aux=wl.alpha, d_z=0.0, out=grads)
+        return time.perf_counter() - t0
+
+    run(32)                        # warm-up: first touch of weights and thread pool
+    t_small = run(64)
+    T = int(max(64, min(wl.T, 64 * seconds / max(t_small, 1e-6))))
+    t = run(T)
+    sample = (f"{T} tokens of the workload shape (H={wl.H}, k={k}, I={wl.I}, S={wl.S}) over "
+              f"{E} experts, oracle fp32 {'fwd+bwd' if wl.backward else 'fwd'}, {threads} threads")
+    return {"value": round(T / t, 2), "unit": "tokens/s", "cores": threads,
+            "kind": "port", "sample": sample, "seconds": round(t, 3)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--seed", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build runs the MoE layer on a single GPU "
+              "(no expert parallelism); --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from oxidizr_amd.moe import MoeConfig, Plan
+    from oxidizr_amd.synth import WORKLOADS
+
+    wl = WORKLOADS[args.config]
+    dev = torch.device("cuda:0")
+    dtype = torch.float32 if wl.dtype == "f32" else torch.bfloat16
+    T, H, E, k, I, S = wl.T, wl.H, wl.E, wl.k, wl.I, wl.S
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(args.seed)
+    x = gen_weights(torch, (T, H), 1.0, gen, dtype, dev)
+    dout = gen_weights(torch, (T, H), 1.0, gen, dtype, dev)
+    router = gen_weights(torch, (E, H), wl.w_std, gen, dtype, dev)
+    gate = gen_weights(torch, (E, I, H), wl.w_std, gen, dtype, dev)
+    up = gen_weights(torch, (E, I, H), wl.w_std, gen, dtype, dev)
+    down = gen_weights(torch, (E, H, I), wl.w_std, gen, dtype, dev)
+    shared = None
+    if S:
+        shared = (gen_weights(torch, (S, H), wl.w_std, gen, dtype, dev),
+                  gen_weights(torch, (S, H), wl.w_std, gen, dtype, dev),
+                  gen_weights(torch, (H, S), wl.w_std, gen, dtype, dev))
+    bias, skew_info = skew_bias(torch, wl, x, router, dev)
+
+    cfg = MoeConfig(hidden_size=H, num_experts=E, experts_per_tok=k, intermediate_size=I,
+                    shared_expert_enabled=S > 0, shared_intermediate_size=S or None,
+                    load_balance_alpha=wl.alpha, router_bias=bias is not None)
+    plan = Plan(cfg, dtype, dev)
+    w, _keep_w = plan.weights_struct(router, list(gate.unbind(0)), list(up.unbind(0)),
+                                     list(down.unbind(0)), bias, shared)
+    out = torch.empty_like(x)
+    aux = torch.empty((), dtype=torch.float32, device=dev)
+    z = torch.empty((), dtype=torch.float32, device=dev)
+    saved = plan.new_saved(T)
+    if wl.backward:
+        dx = torch.empty_like(x)
+        g_router = torch.empty_like(router)
+        g_gate, g_up, g_down = torch.empty_like(gate), torch.empty_like(up), torch.empty_like(down)
+        g_shared = tuple(torch.empty_like(t) for t in shared) if shared else None
+        g, _keep_g = plan.grads_struct(g_router, list(g_gate.unbind(0)), list(g_up.unbind(0)),
+                                       list(g_down.unbind(0)), None, g_shared)
+        d_aux = torch.tensor(float(wl.alpha), device=dev)   # dL/d aux = load_balance_alpha
+        d_z = torch.tensor(0.0, device=dev)                  # z-loss weight 0 in the timed runs
+        has_grad = torch.empty(E, dtype=torch.uint8, device=dev)
+
+    def step():
+        plan.forward(x, w, out=out, saved=saved, aux=aux, z=z)
+        if wl.backward:
+            plan.backward(x, dout, w, g, saved, dx=dx, d_aux=d_aux, d_z=d_z, has_grad=has_grad)
+
+    dominant = "gateup_fwd"
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    counts = plan.saved_field(saved, T, "counts").cpu()
+    plan.stage_times(reset=True)
+    plan.set_profiling([dominant])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    dom_ms, dom_calls = plan.stage_times(reset=True)[dominant]
+    # per-stage breakdown from a few extra (untimed) steps with every stage evented
+    plan.set_profiling(None)
+    for _ in range(3):
+        step()
+    stages = {n: ms / c for n, (ms, c) in plan.stage_times(reset=True).items() if c}
+    plan.set_profiling([])
+
+    ms_per_step = elapsed * 1e3 / args.steps
+    tok_s = T / (elapsed / args.steps)
+    TK = T * k
+    fwd_flops = 2 * T * H * E + 6 * TK * H * I + 6 * T * H * S
+    total_flops = fwd_flops * (3 if wl.backward else 1)
+    dom_avg_ms = dom_ms / max(dom_calls, 1)
+    n_touched = int((counts > 0).sum())
+    if wl.dtype == "f32":
+        peak, bound = PEAK_FP32_TFLOPS, "mfma"
+    else:
+        peak, bound = PEAK_BF16_TFLOPS, "mfma"
+    dom_flops = 4 * TK * H * I
+    if not wl.backward:  # small-token forward: HBM bound on the expert weights touched
+        b = 2
+        dom_bytes = n_touched * 2 * H * I * b + TK * H * b + 3 * TK * I * b
+        roof = {"bound": "hbm", "achieved": round(dom_bytes / (dom_avg_ms * 1e-3) / 1e9, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+        roof["frac"] = round(roof["achieved"] / PEAK_HBM_GBS, 4)
+        layer_bytes = (n_touched * 3 * H * I * b + E * H * b + 2 * T * H * b + T * E * 4 + TK * 8)
+        extra = {"layer_hbm_GBs": round(layer_bytes / (elapsed / args.steps) / 1e9, 1),
+                 "layer_hbm_frac": round(layer_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4)}
+    else:
+        ach = dom_flops / (dom_avg_ms * 1e-3) / 1e12
+        roof = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
+                "frac": round(ach / peak, 4)}
+        extra = {}
+    roof["traffic"] = None
+    roof["kernel"] = f"k_gateup_fwd (grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch"
+
+    gemm_stages = ("gateup_fwd", "down_fwd", "shared_fwd", "down_dgrad", "down_wgrad",
+                   "gateup_dgrad", "gateup_wgrad", "shared_bwd", "router_gemm", "dx")
+    gemm_ms = sum(stages.get(s, 0.0) for s in gemm_stages)
+    res = {
+        "metric": "MoE layer fwd+bwd tokens/sec on 1 MI355X" if wl.backward
+                  else "MoE layer fwd tokens/sec on 1 MI355X",
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16" if wl.dtype == "bf16" else "fp32",
+        "data": "synthetic (seeded N(0,1) tokens, N(0,std) random-init weights)",
+        "config": {"workload": wl.name, "tokens": T, "hidden": H, "num_experts": E,
+                   "experts_per_tok": k, "intermediate": I, "shared_intermediate": S,
+                   "load_balance_alpha": wl.alpha, "pass": "fwd+bwd" if wl.backward else "fwd",
+                   "parallelism": "single GPU", "routing": wl.skew, **skew_info,
+                   "max_expert_tokens": int(counts.max()), "empty_experts": int((counts == 0).sum())},
+        "roofline": roof,
+        "layer_tflops": round(total_flops / (elapsed / args.steps) / 1e12, 1),
+        "layer_mfma_frac": round(total_flops / (elapsed / args.steps) / 1e12 / peak, 4),
+        "gemm_tflops": round(total_flops / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
+        "stages_ms": {n: round(v, 4) for n, v in stages.items()},
+        **extra,
+    }
+    if args.cpu_baseline == "on":
+        try:
+            threads = min(16, len(os.sched_getaffinity(0)))
+        except AttributeError:
+            threads = min(16, os.cpu_count() or 1)
+        res["cpu_baseline"] = cpu_baseline(wl, args.cpu_seconds, threads)
+    else:
+        res["cpu_baseline"] = None
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

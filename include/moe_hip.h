@@ -156,7 +156,9 @@ typedef enum {
 moe_status moe_saved_field_range(const moe_plan* plan, int64_t num_tokens, int32_t field,
                                  size_t* offset, size_t* bytes);
 
-/* Per-stage device timing with HIP events (off by default). */
+/* Per-stage device timing with HIP events recorded on the call's stream
+ * around each stage whose bit (1 << moe_stage) is set in stage_mask; -1 times
+ * every stage, 0 (the default) none. */
 typedef enum {
   MOE_STAGE_ROUTER_GEMM = 0, MOE_STAGE_ROUTE, MOE_STAGE_DISPATCH, MOE_STAGE_GATHER,
   MOE_STAGE_GATEUP_FWD, MOE_STAGE_DOWN_FWD, MOE_STAGE_SHARED_FWD, MOE_STAGE_COMBINE_FWD,
@@ -165,7 +167,7 @@ typedef enum {
   MOE_STAGE_DX, MOE_NUM_STAGES
 } moe_stage;
 const char* moe_stage_name(int32_t stage);
-moe_status moe_plan_set_profiling(moe_plan* plan, int32_t enable);
+moe_status moe_plan_set_profiling(moe_plan* plan, int32_t stage_mask);
 /* Synchronises the pending events, then returns the accumulated milliseconds
  * and launch counts per stage since the last reset (arrays of MOE_NUM_STAGES). */
 moe_status moe_plan_stage_times(moe_plan* plan, float* ms, int32_t* calls, int32_t reset);

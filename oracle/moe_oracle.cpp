@@ -60,10 +60,10 @@ inline R dsilu(R g) {  // d/dg [g * sigmoid(g)]
 // Fixed summation order: 8 interleaved partial sums over k, then summed in order.
 template <typename R>
 void gemm_nt(int M, int N, int K, const R* A, int lda, const R* B, int ldb, R* C, int ldc) {
-#pragma omp parallel for schedule(static)
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m) {
-    const R* a = A + (size_t)m * lda;
     for (int n = 0; n < N; ++n) {
+      const R* a = A + (size_t)m * lda;
       const R* b = B + (size_t)n * ldb;
       R acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
       int k = 0;
@@ -78,31 +78,41 @@ void gemm_nt(int M, int N, int K, const R* A, int lda, const R* B, int ldb, R* C
 }
 
 // C[m, n] = sum_k A[m, k] * B[k, n]; A is [M, K], B is [K, N]. k ascending.
+// Parallel over rows and 256-wide column blocks.
 template <typename R>
 void gemm_nn(int M, int N, int K, const R* A, int lda, const R* B, int ldb, R* C, int ldc) {
-#pragma omp parallel for schedule(static)
+  const int NB = (N + 255) / 256;
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m) {
-    R* c = C + (size_t)m * ldc;
-    for (int n = 0; n < N; ++n) c[n] = 0;
-    for (int k = 0; k < K; ++k) {
-      R a = A[(size_t)m * lda + k];
-      const R* b = B + (size_t)k * ldb;
-      for (int n = 0; n < N; ++n) c[n] += a * b[n];
+    for (int nb = 0; nb < NB; ++nb) {
+      const int n0 = nb * 256, n1 = std::min(N, n0 + 256);
+      R* c = C + (size_t)m * ldc;
+      for (int n = n0; n < n1; ++n) c[n] = 0;
+      for (int k = 0; k < K; ++k) {
+        R a = A[(size_t)m * lda + k];
+        const R* b = B + (size_t)k * ldb;
+        for (int n = n0; n < n1; ++n) c[n] += a * b[n];
+      }
     }
   }
 }
 
 // C[m, n] = sum_k A[k, m] * B[k, n]; A is [K, M], B is [K, N]. k ascending.
+// Parallel over rows and 256-wide column blocks.
 template <typename R>
 void gemm_tn(int M, int N, int K, const R* A, int lda, const R* B, int ldb, R* C, int ldc) {
-#pragma omp parallel for schedule(static)
+  const int NB = (N + 255) / 256;
+#pragma omp parallel for collapse(2) schedule(static)
   for (int m = 0; m < M; ++m) {
-    R* c = C + (size_t)m * ldc;
-    for (int n = 0; n < N; ++n) c[n] = 0;
-    for (int k = 0; k < K; ++k) {
-      R a = A[(size_t)k * lda + m];
-      const R* b = B + (size_t)k * ldb;
-      for (int n = 0; n < N; ++n) c[n] += a * b[n];
+    for (int nb = 0; nb < NB; ++nb) {
+      const int n0 = nb * 256, n1 = std::min(N, n0 + 256);
+      R* c = C + (size_t)m * ldc;
+      for (int n = n0; n < n1; ++n) c[n] = 0;
+      for (int k = 0; k < K; ++k) {
+        R a = A[(size_t)k * lda + m];
+        const R* b = B + (size_t)k * ldb;
+        for (int n = n0; n < n1; ++n) c[n] += a * b[n];
+      }
     }
   }
 }

@@ -149,12 +149,9 @@ class MoeOracle:
             raise KeyError(name)
         return dst[0] if name in ("aux", "z") else dst
 
-    def backward(self, dout, d_aux=0.0, d_z=0.0, fill=np.nan):
-        """Returns a dict of gradients. Experts with no routed token keep the
-        `fill` value in their buffers and report has_grad == 0."""
+    def grad_buffers(self, fill=np.nan):
         c, T = self.cfg, self.T
-        dout = self._c(dout).reshape(T, c.H)
-        g = {
+        return {
             "x": np.empty((T, c.H), self.dt),
             "router": np.empty((c.E, c.H), self.dt),
             "router_bias": np.empty(c.E, self.dt) if c.has_bias else None,
@@ -165,6 +162,14 @@ class MoeOracle:
             "shared_up": np.empty((c.S, c.H), self.dt) if c.S else None,
             "shared_down": np.empty((c.H, c.S), self.dt) if c.S else None,
         }
+
+    def backward(self, dout, d_aux=0.0, d_z=0.0, fill=np.nan, out=None):
+        """Returns a dict of gradients. Experts with no routed token keep the
+        `fill` value in their buffers and report has_grad == 0. `out` may pass
+        buffers from grad_buffers() to reuse."""
+        c, T = self.cfg, self.T
+        dout = self._c(dout).reshape(T, c.H)
+        g = out if out is not None else self.grad_buffers(fill)
         has_grad = np.zeros(c.E, np.uint8)
         lib().oracle_backward(self.h, _ptr(dout), float(d_aux), float(d_z), _ptr(g["x"]),
                               _ptr(g["router"]), _ptr(g["router_bias"]), _ptr(g["gate"]),

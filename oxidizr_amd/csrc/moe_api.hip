@@ -83,7 +83,7 @@ struct moe_plan {
   void** d_tab = nullptr;
   void** h_tab = nullptr;       // pinned host staging
   std::vector<const void*> cached[6];
-  bool profiling = false;
+  uint32_t profile_mask = 0;   // stages timed with HIP events (bit per moe_stage)
   struct Pending { int stage; hipEvent_t a, b; };
   std::vector<Pending> pending;
   std::vector<hipEvent_t> free_events;
@@ -173,7 +173,7 @@ struct StageTimer {
   int stage;
   hipEvent_t a = nullptr;
   StageTimer(moe_plan* p_, hipStream_t s_, int st) : p(p_), s(s_), stage(st) {
-    if (p->profiling) {
+    if ((p->profile_mask >> st) & 1u) {
       a = p->event();
       if (a) (void)hipEventRecord(a, s);
     }
@@ -737,10 +737,10 @@ const char* moe_stage_name(int32_t stage) {
   return names[stage];
 }
 
-moe_status moe_plan_set_profiling(moe_plan* p, int32_t enable) {
+moe_status moe_plan_set_profiling(moe_plan* p, int32_t stage_mask) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
-  p->profiling = enable != 0;
+  p->profile_mask = (uint32_t)stage_mask;
   return MOE_OK;
 }
 

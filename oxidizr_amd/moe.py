@@ -219,8 +219,17 @@ class Plan:
                                                      _p(saved), _p(ws)))
         return saved
 
-    def set_profiling(self, on=True):
-        _lib.check(_lib.load().moe_plan_set_profiling(self.h, int(on)))
+    def set_profiling(self, stages=None):
+        """Time the named stages (all when None, none when []) with HIP events."""
+        L = _lib.load()
+        if stages is None:
+            mask = -1
+        else:
+            names = [L.moe_stage_name(i).decode() for i in range(_lib.NUM_STAGES)]
+            mask = 0
+            for s in stages:
+                mask |= 1 << names.index(s)
+        _lib.check(L.moe_plan_set_profiling(self.h, mask))
 
     def stage_times(self, reset=True):
         ms = (ctypes.c_float * _lib.NUM_STAGES)()
