@@ -8,18 +8,21 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define MOE_DEV __device__ __forceinline__
 
 MOE_DEV float bf2f(bf16_t v) { return __uint_as_float(((uint32_t)v) << 16); }
 
-// float -> bfloat16, round to nearest even; NaN stays NaN.
-MOE_DEV bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// float -> bfloat16 with gfx950's v_cvt_pk_bf16_f32: round to nearest even,
+// NaN stays NaN.
+MOE_DEV uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2_t));
 }
+MOE_DEV bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 
 // Elements of T in one 16-byte vector.
 template <typename T> struct Vec16;
@@ -48,10 +51,10 @@ MOE_DEV void unpack16(u32x4 v, float* f, float) {
 }
 MOE_DEV u32x4 pack16(const float* f, bf16_t) {
   u32x4 r;
-  r.x = (uint32_t)f2bf(f[0]) | ((uint32_t)f2bf(f[1]) << 16);
-  r.y = (uint32_t)f2bf(f[2]) | ((uint32_t)f2bf(f[3]) << 16);
-  r.z = (uint32_t)f2bf(f[4]) | ((uint32_t)f2bf(f[5]) << 16);
-  r.w = (uint32_t)f2bf(f[6]) | ((uint32_t)f2bf(f[7]) << 16);
+  r.x = pack_bf16x2(f[0], f[1]);
+  r.y = pack_bf16x2(f[2], f[3]);
+  r.z = pack_bf16x2(f[4], f[5]);
+  r.w = pack_bf16x2(f[6], f[7]);
   return r;
 }
 MOE_DEV u32x4 pack16(const float* f, float) {
@@ -59,6 +62,28 @@ MOE_DEV u32x4 pack16(const float* f, float) {
   r.x = __float_as_uint(f[0]); r.y = __float_as_uint(f[1]);
   r.z = __float_as_uint(f[2]); r.w = __float_as_uint(f[3]);
   return r;
+}
+
+// Raw buffer resources (gfx9-family descriptor word 3).  A load whose offset
+// lies beyond the resource's byte count returns zero.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOobOffset = 0x80000000u;  // beyond every resource (< 2^31 bytes)
+MOE_DEV rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+MOE_DEV u32x4 buf_ld16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Pointers read from device tables are generic to the compiler; these casts
+// keep their accesses on the global path (flat accesses would also count
+// against the LDS wait counter).
+template <typename T> MOE_DEV const __attribute__((address_space(1))) T* gptr(const T* p) {
+  return (const __attribute__((address_space(1))) T*)p;
+}
+template <typename T> MOE_DEV __attribute__((address_space(1))) T* gptr(T* p) {
+  return (__attribute__((address_space(1))) T*)p;
 }
 
 template <typename T> MOE_DEV u32x4 ld16(const T* p) { return *reinterpret_cast<const u32x4*>(p); }

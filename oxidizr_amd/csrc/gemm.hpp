@@ -35,10 +35,13 @@ struct Tiling {
 };
 
 // Source of one operand tile.  K-contiguous: element (r, k) at base + r*ld + k;
-// transposed: at base + k*ld + r.  Rows at or beyond rows_valid are clamped
-// (K-contiguous) or read as zero (transposed); k at or beyond k_valid reads
-// as zero.  For K-contiguous operands k_valid must be a multiple of V; for
-// transposed operands ld must be at least rows_valid rounded up to V.
+// transposed: at base + k*ld + r.  Rows at or beyond rows_valid and k at or
+// beyond k_valid read as zero (rows beyond rows_valid of a transposed operand
+// may also read neighbouring columns of the same matrix: their products only
+// reach output rows the epilogue drops).  For K-contiguous operands k_valid and
+// ld must be multiples of V; for transposed operands ld must be a multiple of V
+// and at least rows_valid rounded up to V.  Every byte the tile can reach lies
+// within 2^31 bytes of base (the host checks operand extents).
 template <typename T>
 struct OpDesc {
   const T* base;
@@ -77,7 +80,11 @@ MOE_DEV void transpose_vv(const u32x4 (&in)[4], u32x4 (&out)[4], float) {
     for (int i = 0; i < 4; ++i) out[c][i] = in[i][c];
 }
 
-// Per-thread staging of one operand tile of R rows between global memory and LDS.
+// Per-thread staging of one operand tile of R rows between global memory and
+// LDS.  Loads are raw buffer loads: the resource covers exactly the operand's
+// readable extent, so out-of-range rows and the K tail come back as zero from
+// the hardware (no per-load branches), the tile base sits in scalar registers
+// and each load needs one 32-bit offset register.
 template <class C, typename T, int R, bool TRANS>
 struct Stager;
 
@@ -85,29 +92,42 @@ template <class C, typename T, int R>
 struct Stager<C, T, R, false> {
   static constexpr int KV = C::BK / C::V;              // vectors per row
   static constexpr int TOTAL = R * KV;
-  static constexpr int PER = (TOTAL + C::THREADS - 1) / C::THREADS;
+  static_assert(TOTAL % C::THREADS == 0, "tile rows must cover the workgroup");
+  static constexpr int PER = TOTAL / C::THREADS;
+  static constexpr int ROWS_STEP = C::THREADS / KV;    // rows between a thread's loads
   u32x4 r[PER];
-  MOE_DEV void load(const OpDesc<T>& d, int k0, int tid) {
+  rsrc_t rs[2];                                        // one per K segment
+  int k_valid[2];
+  uint32_t voff, step;
+  int kcol;
+  MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
+    const int64_t limit = (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
+    return make_rsrc(d.base, (uint32_t)(limit * (int64_t)sizeof(T)));
+  }
+  MOE_DEV void init(const OpDesc<T>& d, int tid) {
+    rs[0] = rs[1] = rsrc_of(d);
+    k_valid[0] = k_valid[1] = d.k_valid;
+    kcol = (tid % KV) * C::V;
+    voff = (uint32_t)(((tid / KV) * d.ld + kcol) * (int64_t)sizeof(T));
+    step = (uint32_t)(ROWS_STEP * d.ld * (int64_t)sizeof(T));
+  }
+  // Second K segment: same ld and rows as the first.
+  MOE_DEV void init_second(const OpDesc<T>& d) {
+    rs[1] = rsrc_of(d);
+    k_valid[1] = d.k_valid;
+  }
+  MOE_DEV void load(int k0, int seg) {
+    const uint32_t soff = (uint32_t)k0 * sizeof(T);
+    const bool kin = k0 + kcol < k_valid[seg];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      int c = tid + i * C::THREADS;
-      int row = c / KV, kv = c % KV;
-      int rr = row < d.rows_valid ? row : d.rows_valid - 1;
-      int k = k0 + kv * C::V;
-      if ((TOTAL % C::THREADS == 0 || c < TOTAL) && k < d.k_valid)
-        r[i] = ld16(d.base + (int64_t)rr * d.ld + k);
-      else
-        r[i] = u32x4{0, 0, 0, 0};
-    }
+    for (int i = 0; i < PER; ++i) r[i] = buf_ld16(rs[seg], kin ? voff + i * step : kOobOffset, soff);
   }
   MOE_DEV void store(T* s, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      int c = tid + i * C::THREADS;
-      if (TOTAL % C::THREADS == 0 || c < TOTAL) {
-        int row = c / KV, kv = c % KV;
-        st16(s + row * C::LDK + kv * C::V, r[i]);
-      }
+      const int c = tid + i * C::THREADS;
+      const int row = c / KV, kv = c % KV;
+      st16(s + row * C::LDK + kv * C::V, r[i]);
     }
   }
 };
@@ -119,28 +139,38 @@ struct Stager<C, T, R, true> {
   static constexpr int TOTAL = RB * KB;
   static constexpr int PER = (TOTAL + C::THREADS - 1) / C::THREADS;
   u32x4 r[PER][V];
-  MOE_DEV void load(const OpDesc<T>& d, int k0, int tid) {
+  rsrc_t rs[2];                                        // one per K segment
+  uint32_t voff, ldb;
+  MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
+    const int rv = (d.rows_valid + V - 1) / V * V;
+    const int64_t limit = (int64_t)(d.k_valid - 1) * d.ld + rv;
+    return make_rsrc(d.base, d.k_valid > 0 ? (uint32_t)(limit * (int64_t)sizeof(T)) : 0u);
+  }
+  MOE_DEV void init(const OpDesc<T>& d, int tid) {
+    rs[0] = rs[1] = rsrc_of(d);
+    const int rb = tid % RB, kb = tid / RB;            // adjacent threads: adjacent rows
+    voff = (uint32_t)(((int64_t)kb * V * d.ld + rb * V) * (int64_t)sizeof(T));
+    ldb = (uint32_t)(d.ld * (int64_t)sizeof(T));
+  }
+  // Second K segment: same ld and rows as the first.
+  MOE_DEV void init_second(const OpDesc<T>& d) { rs[1] = rsrc_of(d); }
+  MOE_DEV void load(int k0, int seg) {
+    const uint32_t soff = (uint32_t)k0 * ldb;
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      int b = tid + i * C::THREADS;
-      int rb = b % RB, kb = b / RB;                    // adjacent threads: adjacent rows
-      bool ok = (TOTAL % C::THREADS == 0 || b < TOTAL) && rb * V < d.rows_valid;
+      if (TOTAL % C::THREADS == 0 || (int)threadIdx.x + i * C::THREADS < TOTAL) {
+        const uint32_t vi = voff + (uint32_t)(i * (C::THREADS / RB) * V) * ldb;
 #pragma unroll
-      for (int j = 0; j < V; ++j) {
-        int k = k0 + kb * V + j;
-        if (ok && k < d.k_valid)
-          r[i][j] = ld16(d.base + (int64_t)k * d.ld + rb * V);
-        else
-          r[i][j] = u32x4{0, 0, 0, 0};
+        for (int j = 0; j < V; ++j) r[i][j] = buf_ld16(rs[seg], vi + j * ldb, soff);
       }
     }
   }
   MOE_DEV void store(T* s, int tid) const {
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      int b = tid + i * C::THREADS;
+      const int b = tid + i * C::THREADS;
       if (TOTAL % C::THREADS == 0 || b < TOTAL) {
-        int rb = b % RB, kb = b / RB;
+        const int rb = b % RB, kb = b / RB;
         u32x4 t[V];
         transpose_vv(r[i], t, T());
 #pragma unroll
@@ -150,61 +180,95 @@ struct Stager<C, T, R, true> {
   }
 };
 
-// LDS elements needed by a main loop with NA A operands and NB B operands.
+// LDS elements of one pipeline stage and of the whole (double-buffered)
+// main loop with NA A operands and NB B operands.
 template <class C, int NA, int NB>
-constexpr int smem_elems() { return (NA * C::BM + NB * C::BN) * C::LDK; }
+constexpr int stage_elems() { return (NA * C::BM + NB * C::BN) * C::LDK; }
+template <class C, int NA, int NB>
+constexpr int smem_elems() { return 2 * stage_elems<C, NA, NB>(); }
 
 // acc[a * NB + b][tn][tm] += B_b-tile x A_a-tile over k in [0, K).
-// Register-prefetch pipeline: the next k-tile is fetched from global memory
-// while the current one is multiplied out of LDS.
+// Two LDS stages: while the waves multiply out of stage kt & 1, the k-tile
+// kt + 1 (fetched into registers one iteration earlier) is written to the
+// other stage and k-tile kt + 2 is fetched from global memory, so each global
+// load has a whole iteration of MFMA work to land and every iteration needs a
+// single barrier.
+//
+// An optional second K segment (a2, b2, K2: same ld and rows as a and b)
+// continues the same pipeline, so sum_k A1 B1 + sum_k A2 B2 runs as one loop.
 template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
 MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
-                      const OpDesc<T> (&b)[NB], int K, T* smem) {
+                      const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2 = nullptr,
+                      const OpDesc<T>* b2 = nullptr, int K2 = 0) {
+  constexpr int STAGE = stage_elems<C, NA, NB>();
+  constexpr int B_OFF = NA * C::BM * C::LDK;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  T* sA = smem;
-  T* sB = smem + NA * C::BM * C::LDK;
   Stager<C, T, C::BM, A_T> sa[NA];
   Stager<C, T, C::BN, B_T> sb[NB];
-  const int nk = (K + C::BK - 1) / C::BK;
-  if (nk == 0) return;
+  const int nk1 = (K + C::BK - 1) / C::BK;
+  const int nk = nk1 + (K2 > 0 ? (K2 + C::BK - 1) / C::BK : 0);
+  if (nk <= 0) return;
 
 #pragma unroll
-  for (int i = 0; i < NA; ++i) sa[i].load(a[i], 0, tid);
+  for (int i = 0; i < NA; ++i) {
+    sa[i].init(a[i], tid);
+    if (K2 > 0) sa[i].init_second(a2[i]);
+  }
 #pragma unroll
-  for (int i = 0; i < NB; ++i) sb[i].load(b[i], 0, tid);
+  for (int i = 0; i < NB; ++i) {
+    sb[i].init(b[i], tid);
+    if (K2 > 0) sb[i].init_second(b2[i]);
+  }
+  auto fetch = [&](int kt) {
+    const int seg = kt >= nk1 ? 1 : 0;
+    const int k0 = (kt - seg * nk1) * C::BK;
 #pragma unroll
-  for (int i = 0; i < NA; ++i) sa[i].store(sA + i * C::BM * C::LDK, tid);
+    for (int i = 0; i < NA; ++i) sa[i].load(k0, seg);
 #pragma unroll
-  for (int i = 0; i < NB; ++i) sb[i].store(sB + i * C::BN * C::LDK, tid);
+    for (int i = 0; i < NB; ++i) sb[i].load(k0, seg);
+  };
+  auto put = [&](T* stage) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i) sa[i].store(stage + i * C::BM * C::LDK, tid);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) sb[i].store(stage + B_OFF + i * C::BN * C::LDK, tid);
+  };
+
+  fetch(0);
+  put(smem);
+  if (nk > 1) fetch(1);
   __syncthreads();
 
   const int frag_row = lane & 31;
   const int frag_k = (lane >> 5) * C::V;
+  constexpr int KSTEPS = C::BK / (2 * C::V);
+  // Fragments of one k-step; two register sets so the LDS reads of step
+  // kk + 1 are in flight while the MFMAs of step kk issue.
+  u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN];
+  auto read_frags = [&](const T* sA, const T* sB, int kk, int set) {
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+#pragma unroll
+      for (int tm = 0; tm < C::TM; ++tm)
+        af[set][i][tm] = *reinterpret_cast<const u32x4*>(
+            sA + i * C::BM * C::LDK + (wm * C::WM + tm * 32 + frag_row) * C::LDK + kk + frag_k);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int tn = 0; tn < C::TN; ++tn)
+        bfr[set][i][tn] = *reinterpret_cast<const u32x4*>(
+            sB + i * C::BN * C::LDK + (wn * C::WN + tn * 32 + frag_row) * C::LDK + kk + frag_k);
+  };
   for (int kt = 0; kt < nk; ++kt) {
-    const bool more = kt + 1 < nk;
-    if (more) {
+    const T* sA = smem + (kt & 1) * STAGE;
+    const T* sB = sA + B_OFF;
+    read_frags(sA, sB, 0, 0);
 #pragma unroll
-      for (int i = 0; i < NA; ++i) sa[i].load(a[i], (kt + 1) * C::BK, tid);
-#pragma unroll
-      for (int i = 0; i < NB; ++i) sb[i].load(b[i], (kt + 1) * C::BK, tid);
-    }
-#pragma unroll
-    for (int kk = 0; kk < C::BK; kk += 2 * C::V) {
-      u32x4 af[NA][C::TM], bfr[NB][C::TN];
-#pragma unroll
-      for (int i = 0; i < NA; ++i)
-#pragma unroll
-        for (int tm = 0; tm < C::TM; ++tm)
-          af[i][tm] = *reinterpret_cast<const u32x4*>(
-              sA + i * C::BM * C::LDK + (wm * C::WM + tm * 32 + frag_row) * C::LDK + kk + frag_k);
-#pragma unroll
-      for (int i = 0; i < NB; ++i)
-#pragma unroll
-        for (int tn = 0; tn < C::TN; ++tn)
-          bfr[i][tn] = *reinterpret_cast<const u32x4*>(
-              sB + i * C::BN * C::LDK + (wn * C::WN + tn * 32 + frag_row) * C::LDK + kk + frag_k);
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KSTEPS) read_frags(sA, sB, (ks + 1) * 2 * C::V, cur ^ 1);
 #pragma unroll
       for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
@@ -213,16 +277,19 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
           for (int tn = 0; tn < C::TN; ++tn)
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
-              mfma_frag(acc[ia * NB + ib][tn][tm], bfr[ib][tn], af[ia][tm], T());
+              mfma_frag(acc[ia * NB + ib][tn][tm], bfr[cur][ib][tn], af[cur][ia][tm], T());
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (kt + 1 < nk) {
+      // stage (kt + 1) & 1 was last read in iteration kt - 1, which every
+      // wave finished before the barrier that closed that iteration
+      put(smem + ((kt + 1) & 1) * STAGE);
+      // keep the next fetch below the stores: hoisting it would need a
+      // second set of staging registers
+      __builtin_amdgcn_sched_barrier(0);
+      if (kt + 2 < nk) fetch(kt + 2);
     }
     __syncthreads();
-    if (more) {
-#pragma unroll
-      for (int i = 0; i < NA; ++i) sa[i].store(sA + i * C::BM * C::LDK, tid);
-#pragma unroll
-      for (int i = 0; i < NB; ++i) sb[i].store(sB + i * C::BN * C::LDK, tid);
-      __syncthreads();
-    }
   }
 }
 
@@ -258,7 +325,83 @@ MOE_DEV void for_each_frag(const f32x16 (&acc)[NACC][C::TN][C::TM], F&& f) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) v[x][i] = acc[x][tn][tm][4 * q + i];
         f(m, n, v);
+        // one 32 x 32 block at a time: keeps the scheduler from moving every
+        // accumulator into VGPRs at once
+        if (q == 3) __builtin_amdgcn_sched_barrier(0);
       }
+}
+
+// LDS floats the row epilogue needs: every wave stages NACC blocks of WM x 32
+// accumulators, rows padded to 36 floats.
+template <class C, int NACC>
+constexpr int epi_lds_floats() { return 4 * NACC * C::WM * 36; }
+
+// Row epilogue: calls f(m_local, n_local, v) with v[x][i] = acc[x] at
+// (m_local, n_local + i) for i < 8, n_local a multiple of 8.  The accumulators
+// of one 32-column block are first written to a wave-private LDS region and
+// read back as rows, so the caller's element-wise work runs on 8 consecutive
+// outputs per lane (16-byte bf16 stores) and only one block's accumulators is
+// in VGPRs at a time.  The LDS must no longer be in use by the main loop (it
+// ends with a barrier); regions are wave-private, so no barrier is needed.
+template <class C, int NACC, class F>
+MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, F&& f) {
+  static_assert(C::WM % 16 == 0, "rows are visited 16 at a time");
+  constexpr int P = 36;  // padded row pitch (floats)
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  float* reg = lds + wave * NACC * C::WM * P;
+#pragma unroll
+  for (int tn = 0; tn < C::TN; ++tn) {  // unrolled: acc is indexed by constants only
+#pragma unroll
+    for (int x = 0; x < NACC; ++x)
+#pragma unroll
+      for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int row = tm * 32 + (lane & 31);
+          const int col = 8 * q + 4 * (lane >> 5);
+          *reinterpret_cast<f32x4*>(reg + (x * C::WM + row) * P + col) =
+              f32x4{acc[x][tn][tm][4 * q], acc[x][tn][tm][4 * q + 1], acc[x][tn][tm][4 * q + 2],
+                    acc[x][tn][tm][4 * q + 3]};
+        }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 2
+    for (int r0 = 0; r0 < C::WM; r0 += 16) {
+      const int row = r0 + (lane >> 2);
+      const int col = (lane & 3) * 8;
+      float v[NACC][8];
+#pragma unroll
+      for (int x = 0; x < NACC; ++x) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + (x * C::WM + row) * P + col);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + (x * C::WM + row) * P + col + 4);
+        v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
+        v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
+      }
+      f(wm * C::WM + row, wn * C::WN + tn * 32 + col, v);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// Store / load 8 consecutive elements (8-element aligned) of one row in global
+// memory.
+MOE_DEV void store8(bf16_t* p, const float* v) {
+  *gptr(reinterpret_cast<u32x4*>(p)) = u32x4{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                             pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7])};
+}
+MOE_DEV void store8(float* p, const float* v) {
+  *gptr(reinterpret_cast<f32x4*>(p)) = f32x4{v[0], v[1], v[2], v[3]};
+  *gptr(reinterpret_cast<f32x4*>(p + 4)) = f32x4{v[4], v[5], v[6], v[7]};
+}
+MOE_DEV void load8(const bf16_t* p, float* v) {
+  const u32x4 w = *gptr(reinterpret_cast<const u32x4*>(p));
+  unpack16(w, v, bf16_t());
+}
+MOE_DEV void load8(const float* p, float* v) {
+  const f32x4 a = *gptr(reinterpret_cast<const f32x4*>(p));
+  const f32x4 b = *gptr(reinterpret_cast<const f32x4*>(p + 4));
+  v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+  v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
 }
 
 // Find the group g with prefix[g] <= t < prefix[g + 1] (prefix[0] = 0).
@@ -271,23 +414,21 @@ MOE_DEV int find_group(const int* prefix, int G, int t) {
   return lo;
 }
 
-// Store 4 consecutive elements (4-element aligned) of one output row.
+// Store / load 4 consecutive elements (4-element aligned) of one row in global
+// memory.
 MOE_DEV void store4(bf16_t* p, const float* v) {
-  uint2 w;
-  w.x = (uint32_t)f2bf(v[0]) | ((uint32_t)f2bf(v[1]) << 16);
-  w.y = (uint32_t)f2bf(v[2]) | ((uint32_t)f2bf(v[3]) << 16);
-  *reinterpret_cast<uint2*>(p) = w;
+  *gptr(reinterpret_cast<u32x2*>(p)) = u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
 }
 MOE_DEV void store4(float* p, const float* v) {
-  *reinterpret_cast<f32x4*>(p) = f32x4{v[0], v[1], v[2], v[3]};
+  *gptr(reinterpret_cast<f32x4*>(p)) = f32x4{v[0], v[1], v[2], v[3]};
 }
 MOE_DEV void load4(const bf16_t* p, float* v) {
-  uint2 w = *reinterpret_cast<const uint2*>(p);
+  const u32x2 w = *gptr(reinterpret_cast<const u32x2*>(p));
   v[0] = __uint_as_float(w.x << 16); v[1] = __uint_as_float(w.x & 0xffff0000u);
   v[2] = __uint_as_float(w.y << 16); v[3] = __uint_as_float(w.y & 0xffff0000u);
 }
 MOE_DEV void load4(const float* p, float* v) {
-  f32x4 w = *reinterpret_cast<const f32x4*>(p);
+  f32x4 w = *gptr(reinterpret_cast<const f32x4*>(p));
   v[0] = w[0]; v[1] = w[1]; v[2] = w[2]; v[3] = w[3];
 }
 

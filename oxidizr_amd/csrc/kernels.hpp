@@ -12,14 +12,31 @@
 #pragma once
 #include <climits>
 #include <cmath>
+#include <type_traits>
 #include "gemm.hpp"
 
 namespace moe {
 
 // ------------------------------------------------------------------ tilings
-template <typename T> struct GemmTiling;
-template <> struct GemmTiling<bf16_t> { using C = Tiling<bf16_t, 128, 128, 64>; };
-template <> struct GemmTiling<float> { using C = Tiling<float, 128, 128, 32>; };
+// One tiling per GEMM role.  bf16 tiles are 256 wide where the operands allow
+// it: a 2 x 2 wave grid then gives every wave a 128 x 128 accumulator block
+// (256 accumulator registers), which halves the LDS bytes read per MFMA
+// against 64 x 64 wave blocks.  The gate/up forward (two B operands) and the
+// paired wgrad (two A operands) halve the other side to keep 256 accumulators.
+// Router-sized GEMMs (one side = E) keep 128 x 128.  fp32 keeps 128 x 128.
+template <typename T> struct Tilings;
+template <> struct Tilings<bf16_t> {
+  using Router = Tiling<bf16_t, 128, 128, 64>;
+  using GateUp = Tiling<bf16_t, 256, 128, 64>;
+  using Big = Tiling<bf16_t, 256, 256, 64>;
+  using WgradPair = Tiling<bf16_t, 128, 256, 64>;
+};
+template <> struct Tilings<float> {
+  using Router = Tiling<float, 128, 128, 32>;
+  using GateUp = Tiling<float, 128, 128, 32>;
+  using Big = Tiling<float, 128, 128, 32>;
+  using WgradPair = Tiling<float, 128, 128, 32>;
+};
 
 // Row-grouped problems: groups split the M dimension (permuted token rows).
 // offsets == nullptr means one dense group of M rows.
@@ -30,11 +47,16 @@ struct RowGroups {
   int M;
 };
 
+// Tile coordinates are workgroup-uniform, but integer division by a runtime
+// value is expanded on the vector ALU; readfirstlane moves the results back to
+// scalar registers so that the address arithmetic built on them stays scalar.
+MOE_DEV int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
 MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, int& row0,
                           int& mv, int& n0) {
   const int nN = (N + BN - 1) / BN;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int mt = id / nN, nt = id % nN;
+  const int mt = uni(id / nN), nt = uni(id % nN);
   n0 = nt * BN;
   if (g.offsets == nullptr) {
     grp = 0;
@@ -43,10 +65,10 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
     return mv > 0;
   }
   if (mt >= g.tile_prefix[g.G]) return false;
-  grp = find_group(g.tile_prefix, g.G, mt);
+  grp = uni(find_group(g.tile_prefix, g.G, mt));
   const int local = (mt - g.tile_prefix[grp]) * BM;
-  row0 = g.offsets[grp] + local;
-  mv = min(BM, g.offsets[grp + 1] - g.offsets[grp] - local);
+  row0 = uni(g.offsets[grp] + local);
+  mv = uni(min(BM, g.offsets[grp + 1] - g.offsets[grp] - local));
   return mv > 0;
 }
 
@@ -63,14 +85,14 @@ MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp,
   const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
   const int per = nM * nN;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  grp = id / per;
-  const int r = id % per;
-  m0 = (r / nN) * BM;
-  n0 = (r % nN) * BN;
+  grp = uni(id / per);
+  const int r = uni(id % per);
+  m0 = uni(r / nN) * BM;
+  n0 = uni(r % nN) * BN;
   if (grp >= g.G) return false;
   if (g.offsets) {
-    krow0 = g.offsets[grp];
-    K = g.offsets[grp + 1] - krow0;
+    krow0 = uni(g.offsets[grp]);
+    K = uni(g.offsets[grp + 1] - krow0);
   } else {
     krow0 = 0;
     K = g.K;
@@ -95,7 +117,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
                                                        const float* __restrict__ bias,
                                                        float* __restrict__ logits, int Tn, int H,
                                                        int E) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename Tilings<T>::Router;
   __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
   RowGroups g{nullptr, nullptr, 1, Tn};
   int grp, row0, mv, n0;
@@ -394,7 +416,7 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
                                                     const T* const* wu_tab, const T* wu_one,
                                                     int H, int N, T* __restrict__ G,
                                                     T* __restrict__ U, T* __restrict__ A) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename Tilings<T>::GateUp;
   __shared__ __align__(16) T smem[smem_elems<C, 1, 2>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
@@ -405,15 +427,16 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
   f32x16 acc[2][C::TN][C::TM];
   zero_acc<C, 2>(acc);
   mainloop<C, T, false, false, 1, 2>(acc, a, b, H, smem);
-  for_each_frag<C, 2>(acc, [&](int m, int n, auto& v) {
+  static_assert(epi_lds_floats<C, 2>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  for_each_row8<C, 2>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= N) return;
-    float act[4];
+    float act[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) act[i] = silu_f(v[0][i]) * v[1][i];
+    for (int i = 0; i < 8; ++i) act[i] = silu_f(v[0][i]) * v[1][i];
     const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
-    store4(G + o, v[0]);
-    store4(U + o, v[1]);
-    store4(A + o, act);
+    store8(G + o, v[0]);
+    store8(U + o, v[1]);
+    store8(A + o, act);
   });
 }
 
@@ -422,7 +445,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
                                                   const T* const* wd_tab, const T* wd_one, int I,
                                                   int H, T* __restrict__ Y) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename Tilings<T>::Big;
   __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
@@ -432,9 +455,10 @@ __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGr
   f32x16 acc[1][C::TN][C::TM];
   zero_acc<C, 1>(acc);
   mainloop<C, T, false, false, 1, 1>(acc, a, b, I, smem);
-  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= H) return;
-    store4(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+    store8(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
   });
 }
 
@@ -528,7 +552,7 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
                                                     const T* __restrict__ G,
                                                     const T* __restrict__ U,
                                                     T* __restrict__ dG, T* __restrict__ dU) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename Tilings<T>::Big;
   __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
@@ -538,21 +562,22 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
   f32x16 acc[1][C::TN][C::TM];
   zero_acc<C, 1>(acc);
   mainloop<C, T, false, true, 1, 1>(acc, a, b, H, smem);
-  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= N) return;
     const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
-    float g[4], u[4], dg[4], du[4];
-    load4(G + o, g);
-    load4(U + o, u);
+    float g[8], u[8], dg[8], du[8];
+    load8(G + o, g);
+    load8(U + o, u);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < 8; ++i) {
       const float da = alpha * v[0][i];
       const float sg = sigmoid_f(g[i]);
       dg[i] = da * u[i] * (sg * (1.0f + g[i] * (1.0f - sg)));
       du[i] = da * (g[i] * sg);
     }
-    store4(dG + o, dg);
-    store4(dU + o, du);
+    store8(dG + o, dg);
+    store8(dU + o, du);
   });
 }
 
@@ -563,7 +588,7 @@ __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
                                                       const T* const* wg_tab, const T* wg_one,
                                                       const T* const* wu_tab, const T* wu_one,
                                                       int I, int H, T* __restrict__ dX) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename Tilings<T>::Big;
   __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
@@ -571,20 +596,16 @@ __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
   const T* wu = pick(wu_tab, wu_one, grp);
   f32x16 acc[1][C::TN][C::TM];
   zero_acc<C, 1>(acc);
-  {
-    OpDesc<T> a[1] = {{dG + (int64_t)row0 * I, I, mv, I}};
-    OpDesc<T> b[1] = {{wg + n0, H, H - n0, I}};
-    mainloop<C, T, false, true, 1, 1>(acc, a, b, I, smem);
-  }
-  __syncthreads();
-  {
-    OpDesc<T> a[1] = {{dU + (int64_t)row0 * I, I, mv, I}};
-    OpDesc<T> b[1] = {{wu + n0, H, H - n0, I}};
-    mainloop<C, T, false, true, 1, 1>(acc, a, b, I, smem);
-  }
-  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+  // one pipelined loop over K = 2I: the dG / Wg segment, then dU / Wu
+  OpDesc<T> a[1] = {{dG + (int64_t)row0 * I, I, mv, I}};
+  OpDesc<T> b[1] = {{wg + n0, H, H - n0, I}};
+  OpDesc<T> a2[1] = {{dU + (int64_t)row0 * I, I, mv, I}};
+  OpDesc<T> b2[1] = {{wu + n0, H, H - n0, I}};
+  mainloop<C, T, false, true, 1, 1>(acc, a, b, I, smem, a2, b2, I);
+  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= H) return;
-    store4(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+    store8(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
   });
 }
 
@@ -598,7 +619,7 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
                                                KGroups groups, int M, int N, float alpha,
                                                T* const* out0_tab, T* out0_one,
                                                T* const* out1_tab, T* out1_one) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename std::conditional<NA == 2, typename Tilings<T>::WgradPair, typename Tilings<T>::Big>::type;
   __shared__ __align__(16) T smem[smem_elems<C, NA, 1>()];
   int grp, krow0, K, m0, n0;
   if (!resolve_k(groups, M, N, C::BM, C::BN, grp, krow0, K, m0, n0)) return;
@@ -612,17 +633,18 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
   T* o0 = pick(out0_tab, out0_one, grp);
   T* o1 = NA == 2 ? pick(out1_tab, out1_one, grp) : nullptr;
   const int mv = min(C::BM, M - m0);
-  for_each_frag<C, NA>(acc, [&](int m, int n, auto& v) {
+  static_assert(epi_lds_floats<C, NA>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  for_each_row8<C, NA>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= N) return;
     const int64_t o = (int64_t)(m0 + m) * N + n0 + n;
-    float r[4];
+    float r[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = alpha * v[0][i];
-    store4(o0 + o, r);
+    for (int i = 0; i < 8; ++i) r[i] = alpha * v[0][i];
+    store8(o0 + o, r);
     if constexpr (NA == 2) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] = alpha * v[1][i];
-      store4(o1 + o, r);
+      for (int i = 0; i < 8; ++i) r[i] = alpha * v[1][i];
+      store8(o1 + o, r);
     }
   });
 }
@@ -693,7 +715,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
                                                       const int* __restrict__ inv_perm, int k,
                                                       const T* __restrict__ dxs,
                                                       T* __restrict__ dx) {
-  using C = typename GemmTiling<T>::C;
+  using C = typename Tilings<T>::Router;
   __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
   RowGroups g{nullptr, nullptr, 1, Tn};
   int grp, row0, mv, n0;
@@ -704,25 +726,26 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
   zero_acc<C, 1>(acc);
   mainloop<C, T, false, true, 1, 1>(acc, a, b, Epad, smem);
   const int64_t TK = (int64_t)Tn * k;
-  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= H) return;
     const int t = row0 + m;
-    float r[4], q[4];
+    float r[8], q[8];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r[i] = v[0][i];
+    for (int i = 0; i < 8; ++i) r[i] = v[0][i];
     for (int j = 0; j < k; ++j) {
       int64_t p = inv_perm[(int64_t)t * k + j];
       p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
-      load4(dXp + p * H + n0 + n, q);
+      load8(dXp + p * H + n0 + n, q);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] += q[i];
+      for (int i = 0; i < 8; ++i) r[i] += q[i];
     }
     if (dxs) {
-      load4(dxs + (int64_t)t * H + n0 + n, q);
+      load8(dxs + (int64_t)t * H + n0 + n, q);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) r[i] += q[i];
+      for (int i = 0; i < 8; ++i) r[i] += q[i];
     }
-    store4(dx + (int64_t)t * H + n0 + n, r);
+    store8(dx + (int64_t)t * H + n0 + n, r);
   });
 }
 

@@ -290,7 +290,10 @@ template <typename D>
 moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                         const moe_weights* w, D* out, float* aux, float* z, char* saved,
                         char* ws) {
-  using C = typename GemmTiling<D>::C;
+  using CR = typename Tilings<D>::Router;
+  using CG = typename Tilings<D>::GateUp;
+  using CB = typename Tilings<D>::Big;
+  static_assert(CG::BM == CB::BM, "row-grouped GEMMs share one tile-prefix table");
   const moe_config& c = p->cfg;
   const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
             I = c.intermediate, S = c.shared_intermediate;
@@ -300,7 +303,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
   {
     StageTimer st(p, s, MOE_STAGE_ROUTER_GEMM);
-    const int grid = ceil_div(T, C::BM) * ceil_div(E, C::BN);
+    const int grid = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
     hipLaunchKernelGGL(k_router_logits<D>, dim3(grid), dim3(256), 0, s, x, (const D*)w->router,
                        c.has_router_bias ? w->router_bias : nullptr, logits, T, H, E);
     LAUNCH_CHECK();
@@ -309,7 +312,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   if (r != MOE_OK) return r;
   const int* counts = (const int*)(saved + L.f[MOE_SAVED_COUNTS]);
   const int* offsets = (const int*)(saved + L.f[MOE_SAVED_OFFSETS]);
-  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(C::BM) * (E + 1);
+  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(CB::BM) * (E + 1);
   const int* perm = (const int*)(saved + L.f[MOE_SAVED_PERM]);
   const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
   const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
@@ -327,17 +330,17 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const D* const* tu = (const D* const*)(p->d_tab + E);
   const D* const* td = (const D* const*)(p->d_tab + 2 * E);
   const RowGroups rg{offsets, tprefix, E, 0};
-  const int mtiles_max = ceil_div(TK, C::BM) + E;
+  const int mtiles_max = ceil_div(TK, CB::BM) + E;
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_FWD);
-    const int grid = mtiles_max * ceil_div(I, C::BN);
+    const int grid = mtiles_max * ceil_div(I, CG::BN);
     hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr, tu,
                        nullptr, H, I, G, U, A);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_FWD);
-    const int grid = mtiles_max * ceil_div(H, C::BN);
+    const int grid = mtiles_max * ceil_div(H, CB::BN);
     hipLaunchKernelGGL(k_down_fwd<D>, dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I, H, Y);
     LAUNCH_CHECK();
   }
@@ -349,10 +352,10 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     D* sA = (D*)(saved + L.sA);
     sY = (D*)(ws + W.sY);
     const RowGroups dense{nullptr, nullptr, 1, T};
-    hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(ceil_div(T, C::BM) * ceil_div(S, C::BN)), dim3(256),
+    hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)), dim3(256),
                        0, s, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, H, S, sG, sU, sA);
-    hipLaunchKernelGGL(k_down_fwd<D>, dim3(ceil_div(T, C::BM) * ceil_div(H, C::BN)), dim3(256), 0,
+    hipLaunchKernelGGL(k_down_fwd<D>, dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0,
                        s, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
     LAUNCH_CHECK();
   }
@@ -388,7 +391,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                          const float* d_aux, const float* d_z, const D* x, const moe_weights* w,
                          const char* saved, char* ws, D* dx, const moe_grads* g,
                          uint8_t* has_grad) {
-  using C = typename GemmTiling<D>::C;
+  using CR = typename Tilings<D>::Router;
+  using CB = typename Tilings<D>::Big;
+  using CW = typename Tilings<D>::WgradPair;
   const moe_config& c = p->cfg;
   const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
             I = c.intermediate, S = c.shared_intermediate;
@@ -398,7 +403,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   const WsLayout W = p->ws_layout(T64);
   const int* counts = (const int*)(saved + L.f[MOE_SAVED_COUNTS]);
   const int* offsets = (const int*)(saved + L.f[MOE_SAVED_OFFSETS]);
-  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(C::BM) * (E + 1);
+  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(CB::BM) * (E + 1);
   const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
   const int* idx = (const int*)(saved + L.f[MOE_SAVED_TOPK_IDX]);
   const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
@@ -425,7 +430,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
   const RowGroups rg{offsets, tprefix, E, 0};
   const KGroups kg{offsets, E, 0};
-  const int mtiles_max = ceil_div(TK, C::BM) + E;
+  const int mtiles_max = ceil_div(TK, CB::BM) + E;
   {
     StageTimer st(p, s, MOE_STAGE_COMBINE_BWD);
     hipLaunchKernelGGL(k_combine_bwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, dout, Y, inv,
@@ -434,26 +439,26 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_DGRAD);
-    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(mtiles_max * ceil_div(I, C::BN)), dim3(256), 0, s,
+    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(mtiles_max * ceil_div(I, CB::BN)), dim3(256), 0, s,
                        dY, rg, td, nullptr, H, I, 1.0f, G, U, dG, dU);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_WGRAD);
-    const int grid = E * ceil_div(H, C::BM) * ceil_div(I, C::BN);
+    const int grid = E * ceil_div(H, CB::BM) * ceil_div(I, CB::BN);
     hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
                        (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_DGRAD);
-    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(mtiles_max * ceil_div(H, C::BN)), dim3(256), 0, s,
+    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(mtiles_max * ceil_div(H, CB::BN)), dim3(256), 0, s,
                        dG, dU, rg, tg, nullptr, tu, nullptr, I, H, dXp);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_WGRAD);
-    const int grid = E * ceil_div(I, C::BM) * ceil_div(H, C::BN);
+    const int grid = E * ceil_div(I, CW::BM) * ceil_div(H, CW::BN);
     hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
                        (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr);
     LAUNCH_CHECK();
@@ -470,16 +475,16 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     const float sc = c.shared_expert_scale;
     const RowGroups dense{nullptr, nullptr, 1, T};
     const KGroups kdense{nullptr, 1, T};
-    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(ceil_div(T, C::BM) * ceil_div(S, C::BN)), dim3(256),
+    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
                        0, s, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
-    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(H, C::BM) * ceil_div(S, C::BN)), dim3(256),
+    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(H, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
                        0, s, dout, nullptr, (int64_t)H, sA, (int64_t)S, kdense, H, S, sc, nullptr,
                        (D*)g->shared_down, nullptr, nullptr);
-    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(ceil_div(T, C::BM) * ceil_div(H, C::BN)), dim3(256),
+    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
                        0, s, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, S, H, dxs);
-    hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(ceil_div(S, C::BM) * ceil_div(H, C::BN)), dim3(256),
+    hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(ceil_div(S, CW::BM) * ceil_div(H, CW::BN)), dim3(256),
                        0, s, sdG, sdU, (int64_t)S, x, (int64_t)H, kdense, S, H, 1.0f, nullptr,
                        (D*)g->shared_gate, nullptr, (D*)g->shared_up);
     LAUNCH_CHECK();
@@ -496,7 +501,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     }
     LAUNCH_CHECK();
     const KGroups kdense{nullptr, 1, T};
-    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(E, C::BM) * ceil_div(H, C::BN)), dim3(256),
+    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(E, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
                        0, s, dlt, nullptr, (int64_t)Epad, x, (int64_t)H, kdense, E, H, 1.0f,
                        nullptr, (D*)g->router, nullptr, nullptr);
     if (c.has_router_bias && g->router_bias) {
@@ -511,7 +516,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer st(p, s, MOE_STAGE_DX);
-    hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, C::BM) * ceil_div(H, C::BN)),
+    hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, CR::BM) * ceil_div(H, CR::BN)),
                        dim3(256), 0, s, dlt, Epad, E, (const D*)w->router, T, H, dXp, inv, k, dxs,
                        dx);
     if (has_grad) hipLaunchKernelGGL(k_has_grad, dim3(ceil_div(E, 256)), dim3(256), 0, s, counts, E, has_grad);
