@@ -73,29 +73,39 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
 }
 
 // K-grouped problems (weight gradients): groups split the reduction over
-// token rows.  offsets == nullptr means one group with K rows.
+// token rows.  offsets == nullptr means one group with K rows, which may be
+// split into nsplit fixed chunks of kchunk rows (a multiple of the k-tile):
+// each chunk then produces an fp32 partial tile and k_splitk_reduce adds the
+// chunks in ascending order, so the result does not depend on scheduling.
 struct KGroups {
   const int* offsets;
   int G;
   int K;
+  int nsplit;
+  int kchunk;
 };
 
-MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& krow0,
-                       int& K, int& m0, int& n0) {
+MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& split,
+                       int& krow0, int& K, int& m0, int& n0) {
   const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
   const int per = nM * nN;
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  grp = uni(id / per);
+  const int gs = uni(id / per);   // group (grouped) or split chunk (dense)
   const int r = uni(id % per);
   m0 = uni(r / nN) * BM;
   n0 = uni(r % nN) * BN;
-  if (grp >= g.G) return false;
   if (g.offsets) {
+    grp = gs;
+    split = 0;
+    if (grp >= g.G) return false;
     krow0 = uni(g.offsets[grp]);
     K = uni(g.offsets[grp + 1] - krow0);
   } else {
-    krow0 = 0;
-    K = g.K;
+    grp = 0;
+    split = gs;
+    if (split >= g.nsplit) return false;
+    krow0 = split * g.kchunk;
+    K = min(g.kchunk, g.K - krow0);
   }
   return K > 0;
 }
@@ -618,11 +628,12 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
                                                int64_t ldp, const T* __restrict__ Q, int64_t ldq,
                                                KGroups groups, int M, int N, float alpha,
                                                T* const* out0_tab, T* out0_one,
-                                               T* const* out1_tab, T* out1_one) {
+                                               T* const* out1_tab, T* out1_one,
+                                               float* __restrict__ partial) {
   using C = typename std::conditional<NA == 2, typename Tilings<T>::WgradPair, typename Tilings<T>::Big>::type;
   __shared__ __align__(16) T smem[smem_elems<C, NA, 1>()];
-  int grp, krow0, K, m0, n0;
-  if (!resolve_k(groups, M, N, C::BM, C::BN, grp, krow0, K, m0, n0)) return;
+  int grp, split, krow0, K, m0, n0;
+  if (!resolve_k(groups, M, N, C::BM, C::BN, grp, split, krow0, K, m0, n0)) return;
   OpDesc<T> a[NA];
   a[0] = {P0 + krow0 * ldp + m0, ldp, M - m0, K};
   if constexpr (NA == 2) a[1] = {P1 + krow0 * ldp + m0, ldp, M - m0, K};
@@ -634,6 +645,16 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
   T* o1 = NA == 2 ? pick(out1_tab, out1_one, grp) : nullptr;
   const int mv = min(C::BM, M - m0);
   static_assert(epi_lds_floats<C, NA>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  if (groups.nsplit > 1) {  // fp32 partial tile of this chunk, [NA][nsplit][M][N]
+    const int64_t MN = (int64_t)M * N;
+    for_each_row8<C, NA>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+      if (m >= mv || n0 + n >= N) return;
+      const int64_t o = (int64_t)(m0 + m) * N + n0 + n;
+#pragma unroll
+      for (int x = 0; x < NA; ++x) store8(partial + ((int64_t)x * groups.nsplit + split) * MN + o, v[x]);
+    });
+    return;
+  }
   for_each_row8<C, NA>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
     if (m >= mv || n0 + n >= N) return;
     const int64_t o = (int64_t)(m0 + m) * N + n0 + n;
@@ -647,6 +668,27 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
       store8(o1 + o, r);
     }
   });
+}
+
+// out_x[i] = alpha * sum_s partial[x][s][i], s ascending; 8 elements per thread.
+template <typename T>
+__global__ __launch_bounds__(256) void k_splitk_reduce(const float* __restrict__ partial,
+                                                       int nsplit, int64_t MN, float alpha,
+                                                       T* __restrict__ out0, T* __restrict__ out1) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i >= MN) return;
+  const int x = blockIdx.y;
+  T* out = x == 0 ? out0 : out1;
+  float acc[8], v[8];
+  load8(partial + (int64_t)x * nsplit * MN + i, acc);
+  for (int s = 1; s < nsplit; ++s) {
+    load8(partial + ((int64_t)x * nsplit + s) * MN + i, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += v[e];
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] *= alpha;
+  store8(out + i, acc);
 }
 
 // ------------------------------------------------------------------ router backward

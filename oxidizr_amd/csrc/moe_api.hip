@@ -66,13 +66,51 @@ struct WsLayout {
   // forward
   size_t block_hist, block_base, colpart, sY;
   // backward
-  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs;
+  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk;
   size_t total;
 };
 
 int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 int round8(int v) { return (v + 7) / 8 * 8; }
+
+// Split of a dense (all-token) weight gradient over K = tokens: enough fixed
+// chunks for about two rounds of workgroups on 256 CUs, each chunk at least
+// four k-tiles.  The split depends only on the shapes, never on timing.
+struct SplitPlan {
+  int nsplit, kchunk;
+};
+template <class C>
+SplitPlan plan_split(int M, int N, int K) {
+  const int tiles = ceil_div(M, C::BM) * ceil_div(N, C::BN);
+  const int want = ceil_div(512, tiles);
+  const int most = K / (4 * C::BK) > 1 ? K / (4 * C::BK) : 1;
+  int ns = want < most ? want : most;
+  if (ns < 1) ns = 1;
+  const int chunk = ceil_div(ceil_div(K, ns), C::BK) * C::BK;
+  return {ceil_div(K, chunk), chunk};
+}
+
+// fp32 partial-tile bytes of the largest dense weight gradient of one backward.
+template <typename D>
+size_t splitk_bytes(const moe_config& c, int64_t T) {
+  using CB = typename Tilings<D>::Big;
+  using CW = typename Tilings<D>::WgradPair;
+  const int H = c.hidden, E = c.num_experts, S = c.shared_intermediate;
+  size_t most = 0;
+  auto need = [&](SplitPlan sp, int na, int M, int N) {
+    if (sp.nsplit > 1) {
+      const size_t b = (size_t)na * sp.nsplit * (size_t)M * N * 4;
+      if (b > most) most = b;
+    }
+  };
+  need(plan_split<CB>(E, H, (int)T), 1, E, H);
+  if (S > 0) {
+    need(plan_split<CB>(H, S, (int)T), 1, H, S);
+    need(plan_split<CW>(S, H, (int)T), 2, S, H);
+  }
+  return most;
+}
 
 }  // namespace
 
@@ -148,6 +186,8 @@ struct moe_plan {
     L.sdG = g.take(b * T * S);
     L.sdU = g.take(b * T * S);
     L.dxs = g.take(b * T * H);
+    L.splitk = g.take(cfg.dtype == MOE_DTYPE_F32 ? splitk_bytes<float>(cfg, T)
+                                                 : splitk_bytes<bf16_t>(cfg, T));
     L.total = f.off > g.off ? f.off : g.off;
     return L;
   }
@@ -283,6 +323,26 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
 int tile_slot(int bm) {
   switch (bm) {
     case 16: return 0; case 32: return 1; case 64: return 2; case 128: return 3; default: return 4;
+  }
+}
+
+// Weight gradient of a dense (all-token) GEMM: out_x[m, n] = alpha * sum_t
+// P_x[t, m] Q[t, n], split over tokens when that fills the GPU better.
+template <typename D, int NA>
+void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, const D* Q,
+                        int64_t ldq, int T, int M, int N, float alpha, D* o0, D* o1,
+                        float* partial) {
+  using C = typename std::conditional<NA == 2, typename Tilings<D>::WgradPair,
+                                      typename Tilings<D>::Big>::type;
+  const SplitPlan sp = plan_split<C>(M, N, T);
+  const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk};
+  const int tiles = ceil_div(M, C::BM) * ceil_div(N, C::BN);
+  hipLaunchKernelGGL((k_wgrad<D, NA>), dim3(tiles * sp.nsplit), dim3(256), 0, s, P0, P1, ldp, Q,
+                     ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
+  if (sp.nsplit > 1) {
+    const int64_t MN = (int64_t)M * N;
+    hipLaunchKernelGGL(k_splitk_reduce<D>, dim3(ceil_div(MN, 2048), NA), dim3(256), 0, s, partial,
+                       sp.nsplit, MN, alpha, o0, o1);
   }
 }
 
@@ -429,7 +489,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdu = (D* const*)(p->d_tab + 4 * E);
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
   const RowGroups rg{offsets, tprefix, E, 0};
-  const KGroups kg{offsets, E, 0};
+  const KGroups kg{offsets, E, 0, 1, 0};
+  float* partial = (float*)(ws + W.splitk);
   const int mtiles_max = ceil_div(TK, CB::BM) + E;
   {
     StageTimer st(p, s, MOE_STAGE_COMBINE_BWD);
@@ -447,7 +508,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     StageTimer st(p, s, MOE_STAGE_DOWN_WGRAD);
     const int grid = E * ceil_div(H, CB::BM) * ceil_div(I, CB::BN);
     hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
-                       (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr);
+                       (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
   }
   {
@@ -460,7 +521,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     StageTimer st(p, s, MOE_STAGE_GATEUP_WGRAD);
     const int grid = E * ceil_div(I, CW::BM) * ceil_div(H, CW::BN);
     hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
-                       (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr);
+                       (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
   D* dxs = nullptr;
@@ -474,19 +535,16 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     dxs = (D*)(ws + W.dxs);
     const float sc = c.shared_expert_scale;
     const RowGroups dense{nullptr, nullptr, 1, T};
-    const KGroups kdense{nullptr, 1, T};
     hipLaunchKernelGGL(k_down_dgrad<D>, dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
                        0, s, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
-    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(H, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
-                       0, s, dout, nullptr, (int64_t)H, sA, (int64_t)S, kdense, H, S, sc, nullptr,
-                       (D*)g->shared_down, nullptr, nullptr);
+    launch_dense_wgrad<D, 1>(s, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
+                             partial);
     hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
                        0, s, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, S, H, dxs);
-    hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(ceil_div(S, CW::BM) * ceil_div(H, CW::BN)), dim3(256),
-                       0, s, sdG, sdU, (int64_t)S, x, (int64_t)H, kdense, S, H, 1.0f, nullptr,
-                       (D*)g->shared_gate, nullptr, (D*)g->shared_up);
+    launch_dense_wgrad<D, 2>(s, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
+                             (D*)g->shared_up, partial);
     LAUNCH_CHECK();
   }
   {
@@ -500,10 +558,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
       default: launch_router_bwd<16, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
     }
     LAUNCH_CHECK();
-    const KGroups kdense{nullptr, 1, T};
-    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(ceil_div(E, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
-                       0, s, dlt, nullptr, (int64_t)Epad, x, (int64_t)H, kdense, E, H, 1.0f,
-                       nullptr, (D*)g->router, nullptr, nullptr);
+    launch_dense_wgrad<D, 1>(s, dlt, nullptr, Epad, x, H, T, E, H, 1.0f, (D*)g->router, nullptr,
+                             partial);
     if (c.has_router_bias && g->router_bias) {
       const int nrb = ceil_div(T, 64);
       float* part = (float*)(ws);  // column partials at workspace offset 0
