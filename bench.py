@@ -40,11 +40,25 @@ def skew_bias(torch, wl, x, router, dev):
     import numpy as np
     from oxidizr_amd.synth import lognormal_bias, zipf_bias
     E, k = wl.E, wl.k
-    if wl.skew == "lognormal":
-        return torch.tensor(lognormal_bias(E, 0.5), device=dev), {}
-    if wl.skew != "zipf":
+    if wl.skew not in ("zipf", "lognormal"):
         return None, {}
     base = (x.float() @ router.float().t())
+    if wl.skew == "lognormal":
+        # target loads: lognormal(0, 0.5) shares of the T*k assignments; the
+        # per-expert logit bias is fitted to the realized top-k counts
+        target = np.exp(lognormal_bias(E, 0.5).astype(np.float64))
+        target = target / target.sum() * (wl.T * k)
+        tgt = torch.tensor(target, dtype=torch.float32, device=dev)
+        b = torch.log(tgt / tgt.mean()) * 0.1
+        for _ in range(60):
+            idx = torch.topk(base + b, k, dim=1).indices
+            c = torch.bincount(idx.flatten(), minlength=E).float()
+            b = b + 0.3 * torch.log((tgt + 1.0) / (c + 1.0))
+        idx = torch.topk(base + b, k, dim=1).indices
+        c = torch.bincount(idx.flatten(), minlength=E).float()
+        lc = torch.log(c.clamp(min=1.0))
+        return b, {"load_log_std": round(float(lc.std()), 3),
+                   "load_max_over_mean": round(float(c.max() / c.mean()), 2)}
     mean = wl.T * k / E
 
     def counts(beta):
@@ -121,9 +135,23 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 launches) and exit: the "
+                         "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
+                          "launches": 5}), flush=True)
+        return
     if args.gpus != 1:
         print("bench.py measures one MI355X: this build runs the MoE layer on a single GPU "
               "(no expert parallelism); --gpus must be 1", file=sys.stderr)

@@ -180,6 +180,122 @@ struct Stager<C, T, R, true> {
   }
 };
 
+// ---------------------------------------------------------------------------
+// Direct-to-LDS path for two K-contiguous operands.  Buffer loads with the LDS
+// modifier stream each 16-byte vector from global memory straight into LDS (no
+// staging registers, no ds_write): one instruction writes 64 lanes x 16 B =
+// 1 KB, i.e. 8 rows of a 128-byte k-tile row.  Rows are unpadded; the 16-byte
+// slot of k-vector kv in row r is kv ^ (r & 7), so the 8 rows one fragment
+// read touches hit 8 different bank groups.  The lane that fills slot s of
+// row r therefore loads k-vector s ^ (r & 7).
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+template <class C, typename T, int R>
+struct DmaStager {
+  static constexpr int KV = C::BK / C::V;  // 16-byte slots per row
+  static_assert(KV == 8, "one 1 KB LDS chunk = 8 rows of 8 slots");
+  static_assert(R % 32 == 0, "4 waves x 8 rows per instruction");
+  static constexpr int PER = R / 32;       // instructions per wave per k-tile
+  rsrc_t rs;
+  uint32_t voff, step;
+  int kcol, k_valid;
+  MOE_DEV void init(const OpDesc<T>& d, int tid) {
+    const int64_t limit = (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
+    rs = make_rsrc(d.base, (uint32_t)(limit * (int64_t)sizeof(T)));
+    const int lane = tid & 63, wave = tid >> 6;
+    const int row = wave * 8 + (lane >> 3);
+    kcol = ((lane & 7) ^ (lane >> 3)) * C::V;
+    voff = (uint32_t)((row * d.ld + kcol) * (int64_t)sizeof(T));
+    step = (uint32_t)(32 * d.ld * (int64_t)sizeof(T));
+    k_valid = d.k_valid;
+  }
+  MOE_DEV void issue(T* tile, int k0) const {
+    const int wave = threadIdx.x >> 6;
+    const uint32_t soff = (uint32_t)k0 * sizeof(T);
+    const bool kin = k0 + kcol < k_valid;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (lds_void_t*)(tile + (i * 32 + wave * 8) * C::BK), 16,
+          kin ? voff + i * step : kOobOffset, soff, 0, 0);
+  }
+};
+
+// acc += B x A over K for K-contiguous operands, two unpadded LDS stages fed
+// by DMA.  Iteration kt waits for its own DMA (issued one iteration earlier),
+// then a barrier makes every wave's part visible and frees the other stage,
+// which receives k-tile kt + 1 while kt is multiplied out.
+template <class C, typename T, int NA, int NB>
+MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
+                          const OpDesc<T> (&b)[NB], int K, T* smem) {
+  constexpr int TILE_A = C::BM * C::BK, TILE_B = C::BN * C::BK;
+  constexpr int STAGE = NA * TILE_A + NB * TILE_B;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  DmaStager<C, T, C::BM> sa[NA];
+  DmaStager<C, T, C::BN> sb[NB];
+  const int nk = (K + C::BK - 1) / C::BK;
+  if (nk <= 0) return;
+#pragma unroll
+  for (int i = 0; i < NA; ++i) sa[i].init(a[i], tid);
+#pragma unroll
+  for (int i = 0; i < NB; ++i) sb[i].init(b[i], tid);
+  auto issue = [&](int kt) {
+    T* st = smem + (kt & 1) * STAGE;
+#pragma unroll
+    for (int i = 0; i < NA; ++i) sa[i].issue(st + i * TILE_A, kt * C::BK);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) sb[i].issue(st + NA * TILE_A + i * TILE_B, kt * C::BK);
+  };
+  issue(0);
+  const int frag_row = lane & 31;
+  const int frag_kv = lane >> 5;
+  constexpr int KSTEPS = C::BK / (2 * C::V);
+  u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN];
+  auto rd = [&](const T* base, int row, int kv) {
+    return *reinterpret_cast<const u32x4*>(base + row * C::BK + ((kv ^ (row & 7)) * C::V));
+  };
+  auto read_frags = [&](const T* sA, const T* sB, int ks, int set) {
+    const int kv = ks * 2 + frag_kv;
+#pragma unroll
+    for (int i = 0; i < NA; ++i)
+#pragma unroll
+      for (int tm = 0; tm < C::TM; ++tm)
+        af[set][i][tm] = rd(sA + i * TILE_A, wm * C::WM + tm * 32 + frag_row, kv);
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int tn = 0; tn < C::TN; ++tn)
+        bfr[set][i][tn] = rd(sB + i * TILE_B, wn * C::WN + tn * 32 + frag_row, kv);
+  };
+  for (int kt = 0; kt < nk; ++kt) {
+    // the compiler does not track LDS-DMA completion: wait explicitly
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (kt + 1 < nk) issue(kt + 1);
+    const T* sA = smem + (kt & 1) * STAGE;
+    const T* sB = sA + NA * TILE_A;
+    read_frags(sA, sB, 0, 0);
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < KSTEPS) read_frags(sA, sB, ks + 1, cur ^ 1);
+#pragma unroll
+      for (int ia = 0; ia < NA; ++ia)
+#pragma unroll
+        for (int ib = 0; ib < NB; ++ib)
+#pragma unroll
+          for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+            for (int tm = 0; tm < C::TM; ++tm)
+              mfma_frag(acc[ia * NB + ib][tn][tm], bfr[cur][ib][tn], af[cur][ia][tm], T());
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  __syncthreads();  // the caller's epilogue reuses the LDS
+}
+
 // LDS elements of one pipeline stage and of the whole (double-buffered)
 // main loop with NA A operands and NB B operands.
 template <class C, int NA, int NB>
@@ -200,6 +316,13 @@ template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
 MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
                       const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2 = nullptr,
                       const OpDesc<T>* b2 = nullptr, int K2 = 0) {
+  if constexpr (!A_T && !B_T) {
+    if (K2 == 0) {
+      static_assert(2 * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
+      mainloop_dma<C, T, NA, NB>(acc, a, b, K, smem);
+      return;
+    }
+  }
   constexpr int STAGE = stage_elems<C, NA, NB>();
   constexpr int B_OFF = NA * C::BM * C::LDK;
   const int tid = threadIdx.x;

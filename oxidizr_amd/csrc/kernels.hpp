@@ -420,7 +420,9 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // ------------------------------------------------------------------ expert GEMMs (forward)
 // G = X Wg^T, U = X Wu^T, A = silu(G) * U for each row group (expert), or for
 // all T rows (shared expert, groups.offsets == nullptr).
-template <typename T>
+// GROUPED: expert row groups (offsets set); otherwise one dense group (a
+// separate instantiation, so profiles tell the two launches apart).
+template <typename T, bool GROUPED>
 __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
                                                     const T* const* wg_tab, const T* wg_one,
                                                     const T* const* wu_tab, const T* wu_one,
@@ -451,7 +453,7 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
 }
 
 // Y = A Wd^T per row group (K = I) or for the dense shared expert.
-template <typename T>
+template <typename T, bool GROUPED>
 __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
                                                   const T* const* wd_tab, const T* wd_one, int I,
                                                   int H, T* __restrict__ Y) {
@@ -555,7 +557,7 @@ __global__ __launch_bounds__(256) void k_combine_bwd(const T* __restrict__ dout,
 // ------------------------------------------------------------------ expert GEMMs (backward)
 // dA = alpha * dY Wd (NN, K = H), then the SwiGLU backward in the epilogue:
 // dG = dA * U * silu'(G), dU = dA * silu(G).
-template <typename T>
+template <typename T, bool GROUPED>
 __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, RowGroups groups,
                                                     const T* const* wd_tab, const T* wd_one,
                                                     int H, int N, float alpha,
@@ -592,7 +594,7 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
 }
 
 // dX = dG Wg + dU Wu (NN, K = I twice) per row group.
-template <typename T>
+template <typename T, bool GROUPED>
 __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
                                                       const T* __restrict__ dU, RowGroups groups,
                                                       const T* const* wg_tab, const T* wg_one,
@@ -623,7 +625,7 @@ __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
 //   W_a[g][m, n] = alpha * sum_r P_a[r, m] * Q[r, n],  r over the group's rows,
 // with NA = 1 (single) or 2 (two P operands sharing Q).  P is [rows, M]
 // (ld = ldp), Q is [rows, N] (ld = ldq), outputs [M, N].
-template <typename T, int NA>
+template <typename T, int NA, bool GROUPED>
 __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
                                                int64_t ldp, const T* __restrict__ Q, int64_t ldq,
                                                KGroups groups, int M, int N, float alpha,

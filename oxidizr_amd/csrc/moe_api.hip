@@ -337,7 +337,7 @@ void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, co
   const SplitPlan sp = plan_split<C>(M, N, T);
   const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk};
   const int tiles = ceil_div(M, C::BM) * ceil_div(N, C::BN);
-  hipLaunchKernelGGL((k_wgrad<D, NA>), dim3(tiles * sp.nsplit), dim3(256), 0, s, P0, P1, ldp, Q,
+  hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(tiles * sp.nsplit), dim3(256), 0, s, P0, P1, ldp, Q,
                      ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
   if (sp.nsplit > 1) {
     const int64_t MN = (int64_t)M * N;
@@ -394,14 +394,14 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_FWD);
     const int grid = mtiles_max * ceil_div(I, CG::BN);
-    hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr, tu,
+    hipLaunchKernelGGL((k_gateup_fwd<D, true>), dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr, tu,
                        nullptr, H, I, G, U, A);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_FWD);
     const int grid = mtiles_max * ceil_div(H, CB::BN);
-    hipLaunchKernelGGL(k_down_fwd<D>, dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I, H, Y);
+    hipLaunchKernelGGL((k_down_fwd<D, true>), dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I, H, Y);
     LAUNCH_CHECK();
   }
   D* sY = nullptr;
@@ -412,10 +412,10 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     D* sA = (D*)(saved + L.sA);
     sY = (D*)(ws + W.sY);
     const RowGroups dense{nullptr, nullptr, 1, T};
-    hipLaunchKernelGGL(k_gateup_fwd<D>, dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)), dim3(256),
+    hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)), dim3(256),
                        0, s, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, H, S, sG, sU, sA);
-    hipLaunchKernelGGL(k_down_fwd<D>, dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0,
+    hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0,
                        s, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
     LAUNCH_CHECK();
   }
@@ -500,27 +500,27 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_DGRAD);
-    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(mtiles_max * ceil_div(I, CB::BN)), dim3(256), 0, s,
+    hipLaunchKernelGGL((k_down_dgrad<D, true>), dim3(mtiles_max * ceil_div(I, CB::BN)), dim3(256), 0, s,
                        dY, rg, td, nullptr, H, I, 1.0f, G, U, dG, dU);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_WGRAD);
     const int grid = E * ceil_div(H, CB::BM) * ceil_div(I, CB::BN);
-    hipLaunchKernelGGL((k_wgrad<D, 1>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
+    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
                        (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_DGRAD);
-    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(mtiles_max * ceil_div(H, CB::BN)), dim3(256), 0, s,
+    hipLaunchKernelGGL((k_gateup_dgrad<D, true>), dim3(mtiles_max * ceil_div(H, CB::BN)), dim3(256), 0, s,
                        dG, dU, rg, tg, nullptr, tu, nullptr, I, H, dXp);
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_WGRAD);
     const int grid = E * ceil_div(I, CW::BM) * ceil_div(H, CW::BN);
-    hipLaunchKernelGGL((k_wgrad<D, 2>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
+    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
                        (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
@@ -535,12 +535,12 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     dxs = (D*)(ws + W.dxs);
     const float sc = c.shared_expert_scale;
     const RowGroups dense{nullptr, nullptr, 1, T};
-    hipLaunchKernelGGL(k_down_dgrad<D>, dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
+    hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
                        0, s, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
     launch_dense_wgrad<D, 1>(s, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
                              partial);
-    hipLaunchKernelGGL(k_gateup_dgrad<D>, dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
+    hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
                        0, s, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, S, H, dxs);
     launch_dense_wgrad<D, 2>(s, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
