@@ -81,6 +81,23 @@ def skew_bias(torch, wl, x, router, dev):
     return b, {"zipf_beta": round(lo, 4)}
 
 
+def measured_traffic(workload):
+    """Bytes per launch recorded in profiles/*.md ("traffic_bytes_per_launch
+    <workload>: <bytes>"), or None."""
+    pdir = os.path.join(ROOT, "profiles")
+    if not os.path.isdir(pdir):
+        return None
+    key = f"traffic_bytes_per_launch {workload}:"
+    for name in sorted(os.listdir(pdir)):
+        if not name.endswith((".md", ".txt")):
+            continue
+        with open(os.path.join(pdir, name)) as f:
+            for line in f:
+                if line.startswith(key):
+                    return int(line[len(key):].strip())
+    return None
+
+
 def cpu_baseline(wl, seconds, threads):
     """The oracle (fp32, OpenMP) on a bounded sample of the same workload."""
     import numpy as np
@@ -253,19 +270,23 @@ def main():
         roof = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(ach / peak, 4)}
         extra = {}
-    roof["traffic"] = None
-    roof["kernel"] = f"k_gateup_fwd (grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch"
+    # HBM-side bytes per launch of this kernel and workload, as measured by the
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel) that
+    # are summarised under profiles/; null when no such measurement exists.
+    roof["traffic"] = measured_traffic(wl.name)
+    roof["kernel"] = (f"k_gateup_fwd<{'bf16' if wl.dtype == 'bf16' else 'f32'}, true> "
+                      f"(grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch")
 
     gemm_stages = ("gateup_fwd", "down_fwd", "shared_fwd", "down_dgrad", "down_wgrad",
                    "gateup_dgrad", "gateup_wgrad", "shared_bwd", "router_gemm", "dx")
     gemm_ms = sum(stages.get(s, 0.0) for s in gemm_stages)
     res = {
-        "metric": "MoE layer fwd+bwd tokens/sec on 1 MI355X" if wl.backward
-                  else "MoE layer fwd tokens/sec on 1 MI355X",
+        "metric": "MoE layer fwd+bwd tokens/sec on 1 MI355X; % bf16 MFMA peak; % HBM peak"
+                  if wl.backward else "MoE layer fwd tokens/sec on 1 MI355X; % HBM peak",
         "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16" if wl.dtype == "bf16" else "fp32",
+        "dtype": "bf16" if wl.dtype == "bf16" else "f32",
         "data": "synthetic (seeded N(0,1) tokens, N(0,std) random-init weights)",
         "config": {"workload": wl.name, "tokens": T, "hidden": H, "num_experts": E,
                    "experts_per_tok": k, "intermediate": I, "shared_intermediate": S,
