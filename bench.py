@@ -274,8 +274,12 @@ def main():
     # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel) that
     # are summarised under profiles/; null when no such measurement exists.
     roof["traffic"] = measured_traffic(wl.name)
-    roof["kernel"] = (f"k_gateup_fwd<{'bf16' if wl.dtype == 'bf16' else 'f32'}, true> "
-                      f"(grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch")
+    if wl.dtype == "bf16" and T <= 64:   # small-token path: weight-streaming kernels
+        roof["kernel"] = (f"k_skinny_fwd<true, false> (gate/up weight stream + SwiGLU), "
+                          f"{dom_avg_ms:.4f} ms/launch")
+    else:
+        roof["kernel"] = (f"k_gateup_fwd<{'bf16' if wl.dtype == 'bf16' else 'f32'}, true> "
+                          f"(grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch")
 
     gemm_stages = ("gateup_fwd", "down_fwd", "shared_fwd", "down_dgrad", "down_wgrad",
                    "gateup_dgrad", "gateup_wgrad", "shared_bwd", "router_gemm", "dx")

@@ -247,14 +247,19 @@ __global__ __launch_bounds__(256) void k_colsum_partial(const float* __restrict_
     part[(int64_t)blockIdx.y * E + e] = ((red[0][c] + red[1][c]) + red[2][c]) + red[3][c];
 }
 
-// out[e] = scale * sum_rb part[rb, e], rb ascending.
+// out[e] = scale * sum_rb part[rb, e]: four running sums over rb = 4 i + j
+// (independent loads stay in flight), added in the fixed order j = 0..3.
 __global__ void k_colsum_final(const float* __restrict__ part, int nrb, int E, float scale,
                                float* __restrict__ out) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e >= E) return;
-  float s = 0.0f;
-  for (int rb = 0; rb < nrb; ++rb) s += part[(int64_t)rb * E + e];
-  out[e] = s * scale;
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  int rb = 0;
+  for (; rb + 4 <= nrb; rb += 4)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] += part[(int64_t)(rb + j) * E + e];
+  for (; rb < nrb; ++rb) s[rb & 3] += part[(int64_t)rb * E + e];
+  out[e] = (((s[0] + s[1]) + s[2]) + s[3]) * scale;
 }
 
 // aux = E (c_sw sum_e f_e P_e + c_sq sum_e P_e^2), z = mean_t lse_t^2.
@@ -272,7 +277,12 @@ __global__ __launch_bounds__(256) void k_losses(const float* __restrict__ P,
     sw += ((float)counts[e] * inv_tk) * p;
     sq += p * p;
   }
-  for (int t = tid; t < Tn; t += 256) zz += lse[t] * lse[t];
+  {
+    float zp[4] = {0.0f, 0.0f, 0.0f, 0.0f};  // independent loads in flight
+    int t = tid, j = 0;
+    for (; t < Tn; t += 256, j = (j + 1) & 3) zp[j] += lse[t] * lse[t];
+    zz = ((zp[0] + zp[1]) + zp[2]) + zp[3];
+  }
   r_sw[tid] = sw; r_sq[tid] = sq; r_z[tid] = zz;
   __syncthreads();
   for (int o = 128; o >= 1; o >>= 1) {
@@ -308,42 +318,74 @@ __global__ __launch_bounds__(256) void k_hist(const int* __restrict__ idx, int T
 constexpr int kNumTileBM = 5;
 __constant__ int kTileBM[kNumTileBM] = {16, 32, 64, 128, 256};
 
+// Inclusive prefix sum across the 64 lanes of a wave.
+MOE_DEV int wave_incl_scan(int v) {
+  const int lane = threadIdx.x & 63;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// One block of 256 threads (E <= 1024).  Counts and per-block bases come from
+// the block histograms; the expert counts are then held in LDS and scanned in
+// parallel (each thread owns E/256 consecutive experts) for the offsets and
+// for the tile prefix of every height in kTileBM.  Integer arithmetic only.
 __global__ __launch_bounds__(256) void k_scan(const int* __restrict__ block_hist, int nb, int E,
                                               int* __restrict__ block_base,
                                               int* __restrict__ counts,
                                               int* __restrict__ offsets,
                                               int* __restrict__ tile_prefix) {
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
+  __shared__ int cnt[1024], offs[1024];
+  __shared__ int wsum[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int e = tid; e < E; e += 256) {
     int run = 0;
     for (int b = 0; b < nb; ++b) {
       const int c = block_hist[(int64_t)b * E + e];
       block_base[(int64_t)b * E + e] = run;
       run += c;
     }
+    cnt[e] = run;
     counts[e] = run;
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
-    int run = 0;
-    offsets[0] = 0;
-    for (int e = 0; e < E; ++e) {
-      run += counts[e];
-      offsets[e + 1] = run;
+  const int per = (E + 255) / 256;  // <= 4
+  const int e0 = tid * per;
+  for (int j = 0; j <= kNumTileBM; ++j) {
+    const int bm = j == 0 ? 1 : kTileBM[j - 1];
+    int v[4], tot = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + i;
+      int c = (i < per && e < E) ? cnt[e] : 0;
+      c = (c + bm - 1) / bm;
+      v[i] = c;
+      tot += c;
     }
-  }
-  if (threadIdx.x >= 32 && threadIdx.x < 32 + kNumTileBM) {
-    const int j = threadIdx.x - 32, bm = kTileBM[j];
-    int* tp = tile_prefix + j * (E + 1);
-    int run = 0;
-    tp[0] = 0;
-    for (int e = 0; e < E; ++e) {
-      run += (counts[e] + bm - 1) / bm;
-      tp[e + 1] = run;
+    const int incl = wave_incl_scan(tot);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    int run = base + incl - tot;
+    int* dst = j == 0 ? offsets : tile_prefix + (j - 1) * (E + 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = e0 + i;
+      if (i < per && e < E) {
+        dst[e] = run;
+        if (j == 0) offs[e] = run;
+        run += v[i];
+      }
     }
+    if (tid == 255) dst[E] = base + incl;
+    __syncthreads();
   }
-  __syncthreads();
-  for (int e = threadIdx.x; e < E; e += blockDim.x) {
-    const int base = offsets[e];
+  for (int e = tid; e < E; e += 256) {
+    const int base = offs[e];
     for (int b = 0; b < nb; ++b) block_base[(int64_t)b * E + e] += base;
   }
 }
@@ -796,6 +838,178 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
 __global__ void k_has_grad(const int* __restrict__ counts, int E, uint8_t* __restrict__ has_grad) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e < E) has_grad[e] = counts[e] > 0 ? 1 : 0;
+}
+
+// ------------------------------------------------------------------ small-token forward
+// With T <= kSkinnyMaxTokens no expert holds more than that many rows, and the
+// forward is a stream of the touched experts' weights.  One wave owns 16 weight
+// rows and multiplies them with every token row of the expert (up to four
+// chunks of 16) using v_mfma_f32_16x16x32_bf16, A = token rows, B = weight
+// rows.  In a 256-wide k-chunk, MFMA step q covers k = 256 kc + 32 q + [0, 32):
+// lane l (row l % 16, group g = l / 16) supplies k-vector 32 q + 8 g of its
+// weight row and of its token row, so the four lanes of a row read 64
+// contiguous bytes per load instruction.  Experts without tokens read
+// no weights.  GATEUP: out0 = G, out1 = U, out2 = silu(G) * U from W0 = W_g,
+// W1 = W_u; otherwise out0 = X W0^T (down projection).
+constexpr int kSkinnyMaxTokens = 64;
+
+MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+}
+
+// WIDE = false handles the experts with at most 16 tokens (one chunk of token
+// rows), WIDE = true those with 17..64; both are launched and each skips the
+// other's experts.  GATEUP: a workgroup covers 32 intermediate columns; waves 0
+// and 1 stream 16 gate rows each, waves 2 and 3 the matching up rows (one
+// matrix per wave keeps registers low, so more waves keep loads in flight),
+// and the gate accumulators reach the up waves through LDS for the SwiGLU
+// epilogue.  Otherwise (down projection) each of the 4 waves owns 16 rows.
+template <bool GATEUP, bool WIDE>
+__global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X,
+                                                    const int* __restrict__ offsets, int Mdense,
+                                                    const bf16_t* const* w0_tab, const bf16_t* w0_one,
+                                                    const bf16_t* const* w1_tab, const bf16_t* w1_one,
+                                                    int K, int N, bf16_t* __restrict__ out0,
+                                                    bf16_t* __restrict__ out1,
+                                                    bf16_t* __restrict__ out2) {
+  constexpr int ROWS_PER_WG = GATEUP ? 32 : 64;
+  constexpr int NC = WIDE ? 4 : 1;
+  __shared__ f32x4 gbuf[GATEUP ? 2 : 1][NC][64];
+  const int nNb = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
+  const int e = uni(blockIdx.x / nNb), nb = uni(blockIdx.x % nNb);
+  const int r0 = offsets ? offsets[e] : 0;
+  const int M = offsets ? offsets[e + 1] - r0 : Mdense;
+  if (M <= 0 || (WIDE ? M <= 16 : M > 16)) return;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int mat = GATEUP ? wave >> 1 : 0;                 // 0: W0 (gate / down), 1: W1 (up)
+  const int n0 = nb * ROWS_PER_WG + (GATEUP ? (wave & 1) : wave) * 16;
+  const int g = lane >> 4, rl = lane & 15;
+  const int nrows = max(0, min(16, N - n0));
+  const bool active = nrows > 0;                           // wave-uniform
+  const bf16_t* wsrc = mat ? pick(w1_tab, w1_one, e) : pick(w0_tab, w0_one, e);
+  const rsrc_t rw = make_rsrc(wsrc + (int64_t)(active ? n0 : 0) * K,
+                              active ? (uint32_t)((int64_t)nrows * K * 2) : 0u);
+  const rsrc_t rx = make_rsrc(X + (int64_t)r0 * K, (uint32_t)((int64_t)M * K * 2));
+  const int nch = (M + 15) / 16;
+  const uint32_t vw = (uint32_t)((rl * K + 8 * g) * 2);
+  f32x4 acc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  if (active) {
+    for (int kc = 0; kc * 256 < K; ++kc) {
+      const uint32_t soff = (uint32_t)kc * 512;
+      u32x4 wa[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const bool kin = kc * 256 + 32 * q + 8 * g < K;
+        wa[q] = buf_ld16(rw, kin ? vw + 64 * q : kOobOffset, soff);
+      }
+#pragma unroll
+      for (int c = 0; c < NC; ++c) {
+        if (c >= nch) break;
+        const uint32_t vx = (uint32_t)(((c * 16 + rl) * K + 8 * g) * 2);
+        u32x4 xa[8];
+#pragma unroll
+        for (int q = 0; q < 8; ++q) {
+          const bool kin = kc * 256 + 32 * q + 8 * g < K;
+          xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
+        }
+#pragma unroll
+        for (int q = 0; q < 8; ++q) mfma16(acc[c], xa[q], wa[q]);
+      }
+    }
+  }
+  // lane holds D[token = 16 c + 4 g + r][row = rl]
+  if constexpr (GATEUP) {
+    if (mat == 0) {
+#pragma unroll
+      for (int c = 0; c < NC; ++c) gbuf[wave][c][lane] = acc[c];
+    }
+    __syncthreads();
+    if (mat == 0) return;
+  }
+  if (!active || rl >= nrows) return;
+  const int n = n0 + rl;
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    if (c >= nch) break;
+    f32x4 gv4 = acc[c];
+    if constexpr (GATEUP) gv4 = gbuf[wave & 1][c][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = c * 16 + 4 * g + r;
+      if (t >= M) continue;
+      const int64_t o = (int64_t)(r0 + t) * N + n;
+      if constexpr (GATEUP) {
+        const float gv = gv4[r], uv = acc[c][r];
+        out0[o] = f2bf(gv);
+        out1[o] = f2bf(uv);
+        out2[o] = f2bf(silu_f(gv) * uv);
+      } else {
+        out0[o] = f2bf(acc[c][r]);
+      }
+    }
+  }
+}
+
+// Router logits for T <= kSkinnyMaxTokens (bf16): a workgroup owns 16
+// experts, its four waves take every fourth 256-wide k-chunk of the hidden
+// dimension (same lane layout as k_skinny_fwd), and the partial sums are added
+// through LDS in wave order.
+__global__ __launch_bounds__(256) void k_router_small(const bf16_t* __restrict__ x,
+                                                      const bf16_t* __restrict__ wr,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ logits, int Tn, int H,
+                                                      int E) {
+  __shared__ f32x4 red[4][4][64];
+  const int e0 = blockIdx.x * 16;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int g = lane >> 4, rl = lane & 15;
+  const int nrows = min(16, E - e0);
+  const rsrc_t rw = make_rsrc(wr + (int64_t)e0 * H, (uint32_t)((int64_t)nrows * H * 2));
+  const rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)Tn * H * 2));
+  const int nch = (Tn + 15) / 16;
+  const uint32_t vw = (uint32_t)((rl * H + 8 * g) * 2);
+  f32x4 acc[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kc = wave; kc * 256 < H; kc += 4) {
+    const uint32_t soff = (uint32_t)kc * 512;
+    u32x4 wa[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const bool kin = kc * 256 + 32 * q + 8 * g < H;
+      wa[q] = buf_ld16(rw, kin ? vw + 64 * q : kOobOffset, soff);
+    }
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if (c >= nch) break;
+      const uint32_t vx = (uint32_t)(((c * 16 + rl) * H + 8 * g) * 2);
+      u32x4 xa[8];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const bool kin = kc * 256 + 32 * q + 8 * g < H;
+        xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
+      }
+#pragma unroll
+      for (int q = 0; q < 8; ++q) mfma16(acc[c], xa[q], wa[q]);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) red[wave][c][lane] = acc[c];
+  __syncthreads();
+  if (wave != 0 || rl >= nrows) return;
+  const int e = e0 + rl;
+  const float b = bias ? bias[e] : 0.0f;
+  for (int c = 0; c < nch; ++c) {
+    const f32x4 v = ((red[0][c][lane] + red[1][c][lane]) + red[2][c][lane]) + red[3][c][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = c * 16 + 4 * g + r;
+      if (t < Tn) logits[(int64_t)t * E + e] = v[r] + b;
+    }
+  }
 }
 
 }  // namespace moe

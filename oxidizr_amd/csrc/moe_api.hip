@@ -363,9 +363,15 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
   {
     StageTimer st(p, s, MOE_STAGE_ROUTER_GEMM);
-    const int grid = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
-    hipLaunchKernelGGL(k_router_logits<D>, dim3(grid), dim3(256), 0, s, x, (const D*)w->router,
-                       c.has_router_bias ? w->router_bias : nullptr, logits, T, H, E);
+    if (std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens) {
+      hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16)), dim3(256), 0, s, (const bf16_t*)x,
+                         (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
+                         logits, T, H, E);
+    } else {
+      const int grid = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
+      hipLaunchKernelGGL(k_router_logits<D>, dim3(grid), dim3(256), 0, s, x, (const D*)w->router,
+                         c.has_router_bias ? w->router_bias : nullptr, logits, T, H, E);
+    }
     LAUNCH_CHECK();
   }
   moe_status r = run_routing<D>(p, s, T64, saved, ws, L, W);
@@ -391,17 +397,42 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const D* const* td = (const D* const*)(p->d_tab + 2 * E);
   const RowGroups rg{offsets, tprefix, E, 0};
   const int mtiles_max = ceil_div(TK, CB::BM) + E;
+  // few tokens: no expert holds more than T rows, stream the weights instead
+  const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   {
     StageTimer st(p, s, MOE_STAGE_GATEUP_FWD);
-    const int grid = mtiles_max * ceil_div(I, CG::BN);
-    hipLaunchKernelGGL((k_gateup_fwd<D, true>), dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr, tu,
-                       nullptr, H, I, G, U, A);
+    if (skinny) {
+      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
+                         (const bf16_t*)xp, offsets, 0, (const bf16_t* const*)tg, nullptr,
+                         (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)G, (bf16_t*)U,
+                         (bf16_t*)A);
+      if (T > 16)
+        hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
+                           (const bf16_t*)xp, offsets, 0, (const bf16_t* const*)tg, nullptr,
+                           (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)G, (bf16_t*)U,
+                           (bf16_t*)A);
+    } else {
+      const int grid = mtiles_max * ceil_div(I, CG::BN);
+      hipLaunchKernelGGL((k_gateup_fwd<D, true>), dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr,
+                         tu, nullptr, H, I, G, U, A);
+    }
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_DOWN_FWD);
-    const int grid = mtiles_max * ceil_div(H, CB::BN);
-    hipLaunchKernelGGL((k_down_fwd<D, true>), dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I, H, Y);
+    if (skinny) {
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, 64)), dim3(256), 0, s,
+                         (const bf16_t*)A, offsets, 0, (const bf16_t* const*)td, nullptr, nullptr,
+                         nullptr, I, H, (bf16_t*)Y, nullptr, nullptr);
+      if (T > 16)
+        hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(E * ceil_div(H, 64)), dim3(256), 0,
+                           s, (const bf16_t*)A, offsets, 0, (const bf16_t* const*)td, nullptr,
+                           nullptr, nullptr, I, H, (bf16_t*)Y, nullptr, nullptr);
+    } else {
+      const int grid = mtiles_max * ceil_div(H, CB::BN);
+      hipLaunchKernelGGL((k_down_fwd<D, true>), dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I,
+                         H, Y);
+    }
     LAUNCH_CHECK();
   }
   D* sY = nullptr;
@@ -411,12 +442,30 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     D* sU = (D*)(saved + L.sU);
     D* sA = (D*)(saved + L.sA);
     sY = (D*)(ws + W.sY);
-    const RowGroups dense{nullptr, nullptr, 1, T};
-    hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)), dim3(256),
-                       0, s, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                       (const D*)w->shared_up, H, S, sG, sU, sA);
-    hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0,
-                       s, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+    if (skinny && T <= 16) {
+      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32)), dim3(256), 0, s,
+                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
+                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
+                         (bf16_t*)sA);
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64)), dim3(256), 0, s,
+                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
+                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
+    } else if (skinny) {
+      hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32)), dim3(256), 0, s,
+                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
+                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
+                         (bf16_t*)sA);
+      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64)), dim3(256), 0, s,
+                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
+                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
+    } else {
+      const RowGroups dense{nullptr, nullptr, 1, T};
+      hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
+                         dim3(256), 0, s, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                         (const D*)w->shared_up, H, S, sG, sU, sA);
+      hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
+                         dim3(256), 0, s, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+    }
     LAUNCH_CHECK();
   }
   {
