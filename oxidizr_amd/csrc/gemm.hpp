@@ -18,6 +18,7 @@
 // slot a lane supplies is the same function of (lane / 32, element) for both
 // operands, so the contraction covers every k exactly once.
 #pragma once
+#include <type_traits>
 #include "common.hpp"
 
 namespace moe {
@@ -181,14 +182,30 @@ struct Stager<C, T, R, true> {
 };
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS path for two K-contiguous operands.  Buffer loads with the LDS
-// modifier stream each 16-byte vector from global memory straight into LDS (no
-// staging registers, no ds_write): one instruction writes 64 lanes x 16 B =
-// 1 KB, i.e. 8 rows of a 128-byte k-tile row.  Rows are unpadded; the 16-byte
-// slot of k-vector kv in row r is kv ^ (r & 7), so the 8 rows one fragment
-// read touches hit 8 different bank groups.  The lane that fills slot s of
-// row r therefore loads k-vector s ^ (r & 7).
+// Direct-to-LDS path.  Buffer loads with the LDS modifier stream 16-byte
+// vectors from global memory straight into LDS (no staging registers, no
+// ds_write); one instruction writes 64 lanes x 16 B = 1 KB of LDS.
+//
+// K-contiguous operand tile: R rows of BK k, unpadded 128-byte rows; the
+// 16-byte slot of k-vector kv in row r sits at kv ^ (r & 7), so the 8 rows one
+// fragment read touches hit 8 different bank groups.  The lane that fills
+// slot s of row r therefore loads k-vector s ^ (r & 7).
+//
+// K-major operand tile (bf16 only; element (r, k) at base + k*ld + r): BK
+// k-rows of R contiguous columns; the 16-byte slot p of k-row k sits at
+// p ^ tr_swz(k).  Fragments come from ds_read_b64_tr_b16: within each group of
+// 16 lanes, lane 4i + j receives in slot q element j of the 8-byte chunk
+// addressed by lane 4q + i.  When lane 4q + i of group b addresses k-row
+// kk + 8 (b >> 1) + q at column c0 + 16 (b & 1) + 4i, lane L receives the four
+// k = kk + 8 (b >> 1) + [0, 4) of column c0 + (L % 32); a second read at k + 4
+// completes the 8 consecutive k an MFMA lane supplies.
 typedef __attribute__((address_space(3))) void lds_void_t;
+typedef short i16x4_t __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
+
+// 16-byte slot swizzle of the K-major tiles: the four k-rows one transposing
+// read touches land on four different slot pairs.
+MOE_DEV int tr_swz(int k) { return (k & 3) << 1; }
 
 template <class C, typename T, int R>
 struct DmaStager {
@@ -196,78 +213,150 @@ struct DmaStager {
   static_assert(KV == 8, "one 1 KB LDS chunk = 8 rows of 8 slots");
   static_assert(R % 32 == 0, "4 waves x 8 rows per instruction");
   static constexpr int PER = R / 32;       // instructions per wave per k-tile
-  rsrc_t rs;
+  rsrc_t rs[2];                            // one per K segment
+  int k_valid[2];
   uint32_t voff, step;
-  int kcol, k_valid;
-  MOE_DEV void init(const OpDesc<T>& d, int tid) {
+  int kcol;
+  MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
     const int64_t limit = (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
-    rs = make_rsrc(d.base, (uint32_t)(limit * (int64_t)sizeof(T)));
+    return make_rsrc(d.base, (uint32_t)(limit * (int64_t)sizeof(T)));
+  }
+  MOE_DEV void init(const OpDesc<T>& d, int tid) {
+    rs[0] = rs[1] = rsrc_of(d);
+    k_valid[0] = k_valid[1] = d.k_valid;
     const int lane = tid & 63, wave = tid >> 6;
     const int row = wave * 8 + (lane >> 3);
     kcol = ((lane & 7) ^ (lane >> 3)) * C::V;
     voff = (uint32_t)((row * d.ld + kcol) * (int64_t)sizeof(T));
     step = (uint32_t)(32 * d.ld * (int64_t)sizeof(T));
-    k_valid = d.k_valid;
   }
-  MOE_DEV void issue(T* tile, int k0) const {
+  MOE_DEV void init_second(const OpDesc<T>& d) {  // same ld and rows as the first
+    rs[1] = rsrc_of(d);
+    k_valid[1] = d.k_valid;
+  }
+  MOE_DEV void issue(T* tile, int k0, int seg) const {
     const int wave = threadIdx.x >> 6;
     const uint32_t soff = (uint32_t)k0 * sizeof(T);
-    const bool kin = k0 + kcol < k_valid;
+    const bool kin = k0 + kcol < k_valid[seg];
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs, (lds_void_t*)(tile + (i * 32 + wave * 8) * C::BK), 16,
+          rs[seg], (lds_void_t*)(tile + (i * 32 + wave * 8) * C::BK), 16,
           kin ? voff + i * step : kOobOffset, soff, 0, 0);
+  }
+  MOE_DEV static u32x4 frag(const T* tile, int row, int kv) {
+    return *reinterpret_cast<const u32x4*>(tile + row * C::BK + ((kv ^ (row & 7)) * C::V));
   }
 };
 
-// acc += B x A over K for K-contiguous operands, two unpadded LDS stages fed
-// by DMA.  Iteration kt waits for its own DMA (issued one iteration earlier),
+template <class C, typename T, int R>
+struct DmaStagerT {
+  static_assert(sizeof(T) == 2, "transposing LDS reads are 16-bit");
+  static constexpr int SPR = R / 8;              // 16-byte slots per k-row
+  static constexpr int RPI = 64 / SPR;           // k-rows per 1 KB instruction
+  static constexpr int PER = C::BK / (4 * RPI);  // instructions per wave per k-tile
+  static_assert(PER >= 1 && C::BK % (4 * RPI) == 0, "k-rows must cover the waves");
+  rsrc_t rs[2];
+  uint32_t voff, ldb;
+  MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
+    const int rv = (d.rows_valid + 7) / 8 * 8;
+    const int64_t limit = (int64_t)(d.k_valid - 1) * d.ld + rv;
+    return make_rsrc(d.base, d.k_valid > 0 ? (uint32_t)(limit * (int64_t)sizeof(T)) : 0u);
+  }
+  MOE_DEV void init(const OpDesc<T>& d, int tid) {
+    rs[0] = rs[1] = rsrc_of(d);
+    const int lane = tid & 63, wave = tid >> 6;
+    const int krow = wave * RPI + lane / SPR;
+    const int src = (lane % SPR) ^ tr_swz(krow);
+    voff = (uint32_t)(((int64_t)krow * d.ld + src * 8) * (int64_t)sizeof(T));
+    ldb = (uint32_t)(d.ld * (int64_t)sizeof(T));
+  }
+  MOE_DEV void init_second(const OpDesc<T>& d) { rs[1] = rsrc_of(d); }
+  MOE_DEV void issue(T* tile, int k0, int seg) const {
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs[seg], (lds_void_t*)(tile + (i * 4 * RPI + wave * RPI) * R), 16,
+          voff + (uint32_t)(i * 4 * RPI) * ldb, (uint32_t)k0 * ldb, 0, 0);
+  }
+  // operand of the fragment whose first column is col0, k-step starting at kk
+  MOE_DEV static u32x4 frag(const T* tile, int col0, int kk) {
+    const int lane = threadIdx.x & 63;
+    const int s = lane & 15, b = lane >> 4;
+    const int q = s >> 2, i = s & 3;
+    const int col = col0 + 16 * (b & 1) + 4 * i;
+    const int k1 = kk + 8 * (b >> 1) + q, k2 = k1 + 4;
+    const T* a1 = tile + k1 * R + (((col >> 3) ^ tr_swz(k1)) << 3) + (col & 7);
+    const T* a2 = tile + k2 * R + (((col >> 3) ^ tr_swz(k2)) << 3) + (col & 7);
+    const i16x4_t v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a1);
+    const i16x4_t v2 = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4_t*)a2);
+    const u32x2 w1 = __builtin_bit_cast(u32x2, v1), w2 = __builtin_bit_cast(u32x2, v2);
+    return u32x4{w1.x, w1.y, w2.x, w2.y};
+  }
+};
+
+// acc += B x A over K with both operands fed by DMA into two unpadded LDS
+// stages.  Iteration kt waits for its own DMA (issued one iteration earlier),
 // then a barrier makes every wave's part visible and frees the other stage,
-// which receives k-tile kt + 1 while kt is multiplied out.
-template <class C, typename T, int NA, int NB>
+// which receives k-tile kt + 1 while kt is multiplied out.  An optional
+// second K segment (a2, b2, K2: same ld and rows) continues the pipeline.
+template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
 MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
-                          const OpDesc<T> (&b)[NB], int K, T* smem) {
+                          const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2,
+                          const OpDesc<T>* b2, int K2) {
   constexpr int TILE_A = C::BM * C::BK, TILE_B = C::BN * C::BK;
   constexpr int STAGE = NA * TILE_A + NB * TILE_B;
+  using SA = typename std::conditional<A_T, DmaStagerT<C, T, C::BM>, DmaStager<C, T, C::BM>>::type;
+  using SB = typename std::conditional<B_T, DmaStagerT<C, T, C::BN>, DmaStager<C, T, C::BN>>::type;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  DmaStager<C, T, C::BM> sa[NA];
-  DmaStager<C, T, C::BN> sb[NB];
-  const int nk = (K + C::BK - 1) / C::BK;
+  SA sa[NA];
+  SB sb[NB];
+  const int nk1 = (K + C::BK - 1) / C::BK;
+  const int nk = nk1 + (K2 > 0 ? (K2 + C::BK - 1) / C::BK : 0);
   if (nk <= 0) return;
 #pragma unroll
-  for (int i = 0; i < NA; ++i) sa[i].init(a[i], tid);
+  for (int i = 0; i < NA; ++i) {
+    sa[i].init(a[i], tid);
+    if (K2 > 0) sa[i].init_second(a2[i]);
+  }
 #pragma unroll
-  for (int i = 0; i < NB; ++i) sb[i].init(b[i], tid);
+  for (int i = 0; i < NB; ++i) {
+    sb[i].init(b[i], tid);
+    if (K2 > 0) sb[i].init_second(b2[i]);
+  }
   auto issue = [&](int kt) {
+    const int seg = kt >= nk1 ? 1 : 0;
+    const int k0 = (kt - seg * nk1) * C::BK;
     T* st = smem + (kt & 1) * STAGE;
 #pragma unroll
-    for (int i = 0; i < NA; ++i) sa[i].issue(st + i * TILE_A, kt * C::BK);
+    for (int i = 0; i < NA; ++i) sa[i].issue(st + i * TILE_A, k0, seg);
 #pragma unroll
-    for (int i = 0; i < NB; ++i) sb[i].issue(st + NA * TILE_A + i * TILE_B, kt * C::BK);
+    for (int i = 0; i < NB; ++i) sb[i].issue(st + NA * TILE_A + i * TILE_B, k0, seg);
   };
   issue(0);
   const int frag_row = lane & 31;
   const int frag_kv = lane >> 5;
   constexpr int KSTEPS = C::BK / (2 * C::V);
   u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN];
-  auto rd = [&](const T* base, int row, int kv) {
-    return *reinterpret_cast<const u32x4*>(base + row * C::BK + ((kv ^ (row & 7)) * C::V));
-  };
   auto read_frags = [&](const T* sA, const T* sB, int ks, int set) {
     const int kv = ks * 2 + frag_kv;
 #pragma unroll
     for (int i = 0; i < NA; ++i)
 #pragma unroll
-      for (int tm = 0; tm < C::TM; ++tm)
-        af[set][i][tm] = rd(sA + i * TILE_A, wm * C::WM + tm * 32 + frag_row, kv);
+      for (int tm = 0; tm < C::TM; ++tm) {
+        if constexpr (A_T) af[set][i][tm] = SA::frag(sA + i * TILE_A, wm * C::WM + tm * 32, ks * 16);
+        else af[set][i][tm] = SA::frag(sA + i * TILE_A, wm * C::WM + tm * 32 + frag_row, kv);
+      }
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int tn = 0; tn < C::TN; ++tn)
-        bfr[set][i][tn] = rd(sB + i * TILE_B, wn * C::WN + tn * 32 + frag_row, kv);
+      for (int tn = 0; tn < C::TN; ++tn) {
+        if constexpr (B_T) bfr[set][i][tn] = SB::frag(sB + i * TILE_B, wn * C::WN + tn * 32, ks * 16);
+        else bfr[set][i][tn] = SB::frag(sB + i * TILE_B, wn * C::WN + tn * 32 + frag_row, kv);
+      }
   };
   for (int kt = 0; kt < nk; ++kt) {
     // the compiler does not track LDS-DMA completion: wait explicitly
@@ -316,12 +405,12 @@ template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
 MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
                       const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2 = nullptr,
                       const OpDesc<T>* b2 = nullptr, int K2 = 0) {
-  if constexpr (!A_T && !B_T) {
-    if (K2 == 0) {
-      static_assert(2 * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
-      mainloop_dma<C, T, NA, NB>(acc, a, b, K, smem);
-      return;
-    }
+  // DMA for every bf16 operand layout; fp32 K-major operands keep the
+  // register-staged transpose below (the transposing LDS read is 16-bit)
+  if constexpr (sizeof(T) == 2 || (!A_T && !B_T)) {
+    static_assert(2 * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
+    mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, a, b, K, smem, a2, b2, K2);
+    return;
   }
   constexpr int STAGE = stage_elems<C, NA, NB>();
   constexpr int B_OFF = NA * C::BM * C::LDK;
