@@ -237,12 +237,16 @@ def main():
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     dom_ms, dom_calls = plan.stage_times(reset=True)[dominant]
-    # per-stage breakdown from a few extra (untimed) steps with every stage evented
+    # per-stage breakdown from a few extra (untimed) steps with every stage
+    # evented and the shared expert in serial order (in the timed steps it runs
+    # concurrently on the plan's second stream, so stage times there overlap)
+    plan.set_shared_overlap(False)
     plan.set_profiling(None)
     for _ in range(3):
         step()
     stages = {n: ms / c for n, (ms, c) in plan.stage_times(reset=True).items() if c}
     plan.set_profiling([])
+    plan.set_shared_overlap(True)
 
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = T / (elapsed / args.steps)
@@ -269,7 +273,9 @@ def main():
         ach = dom_flops / (dom_avg_ms * 1e-3) / 1e12
         roof = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
                 "frac": round(ach / peak, 4)}
-        extra = {}
+        iso = dom_flops / (stages[dominant] * 1e-3) / 1e12
+        extra = {"dominant_kernel_serial": {"achieved": round(iso, 1), "frac": round(iso / peak, 4),
+                                            "ms": round(stages[dominant], 4)}}
     # HBM-side bytes per launch of this kernel and workload, as measured by the
     # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel) that
     # are summarised under profiles/; null when no such measurement exists.

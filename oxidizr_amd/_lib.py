@@ -19,6 +19,7 @@ EXPORTED = [
     "moe_config_default", "moe_plan_create", "moe_plan_destroy", "moe_saved_bytes",
     "moe_workspace_bytes", "moe_forward", "moe_backward", "moe_route_from_logits",
     "moe_saved_field_range", "moe_stage_name", "moe_plan_set_profiling", "moe_plan_stage_times",
+    "moe_plan_set_shared_overlap",
     "moe_last_error", "moe_version",
 ]
 NUM_STAGES = 17
@@ -91,6 +92,8 @@ def load():
     L.moe_stage_name.restype = ctypes.c_char_p
     L.moe_plan_set_profiling.argtypes = [_vp, i32]
     L.moe_plan_set_profiling.restype = i32
+    L.moe_plan_set_shared_overlap.argtypes = [_vp, i32]
+    L.moe_plan_set_shared_overlap.restype = i32
     L.moe_plan_stage_times.argtypes = [_vp, P(ctypes.c_float), P(i32), i32]
     L.moe_plan_stage_times.restype = i32
     L.moe_last_error.argtypes = []

@@ -66,7 +66,7 @@ struct WsLayout {
   // forward
   size_t block_hist, block_base, colpart, sY;
   // backward
-  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk;
+  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared;
   size_t total;
 };
 
@@ -91,9 +91,11 @@ SplitPlan plan_split(int M, int N, int K) {
   return {ceil_div(K, chunk), chunk};
 }
 
-// fp32 partial-tile bytes of the largest dense weight gradient of one backward.
+// fp32 partial-tile bytes of the largest dense weight gradient of one backward:
+// the router's, or the shared expert's (they run concurrently, on separate
+// buffers).
 template <typename D>
-size_t splitk_bytes(const moe_config& c, int64_t T) {
+size_t splitk_bytes(const moe_config& c, int64_t T, bool shared) {
   using CB = typename Tilings<D>::Big;
   using CW = typename Tilings<D>::WgradPair;
   const int H = c.hidden, E = c.num_experts, S = c.shared_intermediate;
@@ -104,8 +106,8 @@ size_t splitk_bytes(const moe_config& c, int64_t T) {
       if (b > most) most = b;
     }
   };
-  need(plan_split<CB>(E, H, (int)T), 1, E, H);
-  if (S > 0) {
+  if (!shared) need(plan_split<CB>(E, H, (int)T), 1, E, H);
+  if (shared && S > 0) {
     need(plan_split<CB>(H, S, (int)T), 1, H, S);
     need(plan_split<CW>(S, H, (int)T), 2, S, H);
   }
@@ -127,6 +129,13 @@ struct moe_plan {
   std::vector<hipEvent_t> free_events;
   float stage_ms[MOE_NUM_STAGES] = {};
   int32_t stage_calls[MOE_NUM_STAGES] = {};
+  // The shared expert does not depend on routing: it runs on a second stream
+  // (default priority), forked from and joined back into the caller's stream
+  // within each call, and fills the routed GEMMs' partial rounds of work.
+  hipStream_t aux = nullptr;
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool overlap = true;
+  hipStream_t shared_stream(hipStream_t s) const { return overlap && aux ? aux : s; }
 
   int E() const { return cfg.num_experts; }
   int es() const { return elt_size(cfg.dtype); }
@@ -186,8 +195,11 @@ struct moe_plan {
     L.sdG = g.take(b * T * S);
     L.sdU = g.take(b * T * S);
     L.dxs = g.take(b * T * H);
-    L.splitk = g.take(cfg.dtype == MOE_DTYPE_F32 ? splitk_bytes<float>(cfg, T)
-                                                 : splitk_bytes<bf16_t>(cfg, T));
+    const bool f32 = cfg.dtype == MOE_DTYPE_F32;
+    L.splitk_router = g.take(f32 ? splitk_bytes<float>(cfg, T, false)
+                                 : splitk_bytes<bf16_t>(cfg, T, false));
+    L.splitk_shared = g.take(f32 ? splitk_bytes<float>(cfg, T, true)
+                                 : splitk_bytes<bf16_t>(cfg, T, true));
     L.total = f.off > g.off ? f.off : g.off;
     return L;
   }
@@ -360,6 +372,47 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const int64_t TK = T64 * k;
   const SavedLayout L = p->saved_layout(T64);
   const WsLayout W = p->ws_layout(T64);
+  // Shared expert first, on the plan's second stream: it only needs x.
+  D* sY = nullptr;
+  const bool skinny_sh = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
+  if (S > 0) {
+    const hipStream_t ss = p->shared_stream(s);
+    if (ss != s) {
+      HIP_TRY(hipEventRecord(p->fork, s));
+      HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
+    }
+    StageTimer st(p, ss, MOE_STAGE_SHARED_FWD);
+    D* sG = (D*)(saved + L.sG);
+    D* sU = (D*)(saved + L.sU);
+    D* sA = (D*)(saved + L.sA);
+    sY = (D*)(ws + W.sY);
+    if (skinny_sh && T <= 16) {
+      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
+                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
+                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
+                         (bf16_t*)sA);
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
+                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
+                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
+    } else if (skinny_sh) {
+      hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
+                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
+                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
+                         (bf16_t*)sA);
+      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
+                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
+                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
+    } else {
+      const RowGroups dense{nullptr, nullptr, 1, T};
+      hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
+                         dim3(256), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                         (const D*)w->shared_up, H, S, sG, sU, sA);
+      hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
+                         dim3(256), 0, ss, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+    }
+    LAUNCH_CHECK();
+    if (ss != s) HIP_TRY(hipEventRecord(p->join, ss));
+  }
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
   {
     StageTimer st(p, s, MOE_STAGE_ROUTER_GEMM);
@@ -435,39 +488,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  D* sY = nullptr;
-  if (S > 0) {
-    StageTimer st(p, s, MOE_STAGE_SHARED_FWD);
-    D* sG = (D*)(saved + L.sG);
-    D* sU = (D*)(saved + L.sU);
-    D* sA = (D*)(saved + L.sA);
-    sY = (D*)(ws + W.sY);
-    if (skinny && T <= 16) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32)), dim3(256), 0, s,
-                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
-                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
-                         (bf16_t*)sA);
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64)), dim3(256), 0, s,
-                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
-                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
-    } else if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32)), dim3(256), 0, s,
-                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
-                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
-                         (bf16_t*)sA);
-      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64)), dim3(256), 0, s,
-                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
-                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
-    } else {
-      const RowGroups dense{nullptr, nullptr, 1, T};
-      hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
-                         dim3(256), 0, s, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                         (const D*)w->shared_up, H, S, sG, sU, sA);
-      hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
-                         dim3(256), 0, s, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
-    }
-    LAUNCH_CHECK();
-  }
+  if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
   {
     StageTimer st(p, s, MOE_STAGE_COMBINE_FWD);
     hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, Y, inv, topw,
@@ -539,8 +560,38 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
   const RowGroups rg{offsets, tprefix, E, 0};
   const KGroups kg{offsets, E, 0, 1, 0};
-  float* partial = (float*)(ws + W.splitk);
+  float* partial = (float*)(ws + W.splitk_router);
   const int mtiles_max = ceil_div(TK, CB::BM) + E;
+  // Shared expert backward first, on the plan's second stream: it needs only
+  // d_out, x and its own saved activations; dx waits for it below.
+  D* dxs = nullptr;
+  if (S > 0) {
+    const hipStream_t ss = p->shared_stream(s);
+    if (ss != s) {
+      HIP_TRY(hipEventRecord(p->fork, s));
+      HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
+    }
+    StageTimer st(p, ss, MOE_STAGE_SHARED_BWD);
+    float* partial_sh = (float*)(ws + W.splitk_shared);
+    const D* sG = (const D*)(saved + L.sG);
+    const D* sU = (const D*)(saved + L.sU);
+    const D* sA = (const D*)(saved + L.sA);
+    D* sdG = (D*)(ws + W.sdG);
+    D* sdU = (D*)(ws + W.sdU);
+    dxs = (D*)(ws + W.dxs);
+    const float sc = c.shared_expert_scale;
+    const RowGroups dense{nullptr, nullptr, 1, T};
+    hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
+                       sdG, sdU);
+    launch_dense_wgrad<D, 1>(ss, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
+                             partial_sh);
+    hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0, ss, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                       (const D*)w->shared_up, S, H, dxs);
+    launch_dense_wgrad<D, 2>(ss, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
+                             (D*)g->shared_up, partial_sh);
+    LAUNCH_CHECK();
+    if (ss != s) HIP_TRY(hipEventRecord(p->join, ss));
+  }
   {
     StageTimer st(p, s, MOE_STAGE_COMBINE_BWD);
     hipLaunchKernelGGL(k_combine_bwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, dout, Y, inv,
@@ -573,29 +624,6 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                        (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
-  D* dxs = nullptr;
-  if (S > 0) {
-    StageTimer st(p, s, MOE_STAGE_SHARED_BWD);
-    const D* sG = (const D*)(saved + L.sG);
-    const D* sU = (const D*)(saved + L.sU);
-    const D* sA = (const D*)(saved + L.sA);
-    D* sdG = (D*)(ws + W.sdG);
-    D* sdU = (D*)(ws + W.sdU);
-    dxs = (D*)(ws + W.dxs);
-    const float sc = c.shared_expert_scale;
-    const RowGroups dense{nullptr, nullptr, 1, T};
-    hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256),
-                       0, s, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
-                       sdG, sdU);
-    launch_dense_wgrad<D, 1>(s, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
-                             partial);
-    hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256),
-                       0, s, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                       (const D*)w->shared_up, S, H, dxs);
-    launch_dense_wgrad<D, 2>(s, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
-                             (D*)g->shared_up, partial);
-    LAUNCH_CHECK();
-  }
   {
     StageTimer st(p, s, MOE_STAGE_ROUTER_BWD);
     const int grid = ceil_div(T, 4);
@@ -619,6 +647,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     }
     LAUNCH_CHECK();
   }
+  if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
   {
     StageTimer st(p, s, MOE_STAGE_DX);
     hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, CR::BM) * ceil_div(H, CR::BN)),
@@ -707,9 +736,14 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
   hipError_t e = hipMalloc((void**)&p->d_tab, tab_bytes);
   if (e == hipSuccess) e = hipHostMalloc((void**)&p->h_tab, tab_bytes, hipHostMallocDefault);
   if (e == hipSuccess) e = hipMemset(p->d_tab, 0, tab_bytes);
+  if (e == hipSuccess && cfg->shared_intermediate > 0) {
+    e = hipStreamCreateWithFlags(&p->aux, hipStreamNonBlocking);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->join, hipEventDisableTiming);
+  }
   if (e != hipSuccess) {
     moe_plan_destroy(p);
-    return fail(e == hipErrorOutOfMemory ? MOE_ERR_OOM : MOE_ERR_HIP, "plan tables: %s",
+    return fail(e == hipErrorOutOfMemory ? MOE_ERR_OOM : MOE_ERR_HIP, "plan set-up: %s",
                 hipGetErrorString(e));
   }
   *out = p;
@@ -724,8 +758,12 @@ moe_status moe_plan_destroy(moe_plan* p) {
     hipEventDestroy(q.b);
   }
   for (auto e : p->free_events) hipEventDestroy(e);
-  if (p->d_tab) hipFree(p->d_tab);
-  if (p->h_tab) hipHostFree(p->h_tab);
+  if (p->aux) (void)hipStreamSynchronize(p->aux);
+  if (p->fork) (void)hipEventDestroy(p->fork);
+  if (p->join) (void)hipEventDestroy(p->join);
+  if (p->aux) (void)hipStreamDestroy(p->aux);
+  if (p->d_tab) (void)hipFree(p->d_tab);
+  if (p->h_tab) (void)hipHostFree(p->h_tab);
   delete p;
   return MOE_OK;
 }
@@ -851,6 +889,13 @@ moe_status moe_plan_set_profiling(moe_plan* p, int32_t stage_mask) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
   p->profile_mask = (uint32_t)stage_mask;
+  return MOE_OK;
+}
+
+moe_status moe_plan_set_shared_overlap(moe_plan* p, int32_t on) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  p->overlap = on != 0;
   return MOE_OK;
 }
 

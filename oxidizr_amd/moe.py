@@ -231,6 +231,11 @@ class Plan:
                 mask |= 1 << names.index(s)
         _lib.check(L.moe_plan_set_profiling(self.h, mask))
 
+    def set_shared_overlap(self, on=True):
+        """Run the shared expert on the plan's second stream (default) or in
+        serial order on the call's stream."""
+        _lib.check(_lib.load().moe_plan_set_shared_overlap(self.h, int(bool(on))))
+
     def stage_times(self, reset=True):
         ms = (ctypes.c_float * _lib.NUM_STAGES)()
         calls = (ctypes.c_int32 * _lib.NUM_STAGES)()

@@ -36,7 +36,8 @@ class Case:
         return f"Case(T={self.T},H={self.H},E={self.E},k={self.k},I={self.I},S={self.S},{self.dtype})"
 
 
-def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x=None):
+def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x=None,
+            overlap=True):
     """Forward (+ backward) on cuda:0. Returns a dict of numpy results."""
     dev = torch.device("cuda:0")
     p = case.p
@@ -49,6 +50,7 @@ def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x
     bias = torch.tensor(p["router_bias"], device=dev) if case.bias is not None else None
     T = t["x"].shape[0]
     plan = Plan(case.cfg, dt, dev)
+    plan.set_shared_overlap(overlap)
     gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
     shared = (t["shared_gate"], t["shared_up"], t["shared_down"]) if case.S else None
     w, _keep = plan.weights_struct(t["router"], gate, up, down, bias, shared)

@@ -192,6 +192,18 @@ def test_bitwise_reproducible(dtype):
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_shared_stream_overlap_is_bitwise_serial(dtype):
+    # the shared expert on the plan's second stream gives the same bits as the
+    # serial order: no result depends on how the two streams interleave
+    case = Case(T=640, H=128, E=16, k=2, I=64, S=128, dtype=dtype, w_std=0.05, seed=5)
+    a = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=True)
+    b = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=False)
+    for n in ("out", "aux", "z", "dx", "router", "gate", "up", "down", "shared_gate",
+              "shared_up", "shared_down"):
+        np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_batch_invariance(dtype):
     # Routing is per token (reference tests/data_parallel.rs:333-347), and no
     # reduction crosses tokens in out or (with d_aux = d_z = 0) in dx: a token's
