@@ -187,9 +187,12 @@ struct Stager<C, T, R, true> {
 // ds_write); one instruction writes 64 lanes x 16 B = 1 KB of LDS.
 //
 // K-contiguous operand tile: R rows of BK k, unpadded 128-byte rows; the
-// 16-byte slot of k-vector kv in row r sits at kv ^ (r & 7), so the 8 rows one
-// fragment read touches hit 8 different bank groups.  The lane that fills
-// slot s of row r therefore loads k-vector s ^ (r & 7).
+// 16-byte slot of k-vector kv in row r sits at kv ^ nt_swz(r).  A fragment
+// read serves 16 consecutive rows per LDS cycle (256 bytes, 64 banks): rows r
+// and r + 8 share a bank window, so the swizzle also depends on bit 3 of r and
+// the 16 rows land on 16 different 16-byte bank groups (the first 8 on 8
+// different ones as well).  The lane that fills slot s of row r therefore
+// loads k-vector s ^ nt_swz(r).
 //
 // K-major operand tile (bf16 only; element (r, k) at base + k*ld + r): BK
 // k-rows of R contiguous columns; the 16-byte slot p of k-row k sits at
@@ -203,9 +206,11 @@ typedef __attribute__((address_space(3))) void lds_void_t;
 typedef short i16x4_t __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 
-// 16-byte slot swizzle of the K-major tiles: the four k-rows one transposing
-// read touches land on four different slot pairs.
-MOE_DEV int tr_swz(int k) { return (k & 3) << 1; }
+// 16-byte slot swizzles.  K-contiguous tiles: see above.  K-major tiles: the 32
+// lanes one transposing read serves per cycle cover slots 0..3 of four
+// consecutive k-rows; XOR-ing by 4 (k & 3) gives them 16 different slots.
+MOE_DEV int nt_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+MOE_DEV int tr_swz(int k) { return (k & 3) << 2; }
 
 template <class C, typename T, int R>
 struct DmaStager {
@@ -225,8 +230,8 @@ struct DmaStager {
     rs[0] = rs[1] = rsrc_of(d);
     k_valid[0] = k_valid[1] = d.k_valid;
     const int lane = tid & 63, wave = tid >> 6;
-    const int row = wave * 8 + (lane >> 3);
-    kcol = ((lane & 7) ^ (lane >> 3)) * C::V;
+    const int row = wave * 8 + (lane >> 3);   // bits 0-3 are the same for every chunk i
+    kcol = ((lane & 7) ^ nt_swz(row)) * C::V;
     voff = (uint32_t)((row * d.ld + kcol) * (int64_t)sizeof(T));
     step = (uint32_t)(32 * d.ld * (int64_t)sizeof(T));
   }
@@ -245,7 +250,7 @@ struct DmaStager {
           kin ? voff + i * step : kOobOffset, soff, 0, 0);
   }
   MOE_DEV static u32x4 frag(const T* tile, int row, int kv) {
-    return *reinterpret_cast<const u32x4*>(tile + row * C::BK + ((kv ^ (row & 7)) * C::V));
+    return *reinterpret_cast<const u32x4*>(tile + row * C::BK + ((kv ^ nt_swz(row)) * C::V));
   }
 };
 
