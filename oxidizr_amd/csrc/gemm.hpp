@@ -345,6 +345,7 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
   const int frag_row = lane & 31;
   const int frag_kv = lane >> 5;
   constexpr int KSTEPS = C::BK / (2 * C::V);
+  static_assert(KSTEPS % 2 == 0, "the next tile's first fragments go to register set 0");
   u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN];
   auto read_frags = [&](const T* sA, const T* sB, int ks, int set) {
     const int kv = ks * 2 + frag_kv;
@@ -363,18 +364,31 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
         else bfr[set][i][tn] = SB::frag(sB + i * TILE_B, wn * C::WN + tn * 32 + frag_row, kv);
       }
   };
+  // The compiler does not track LDS-DMA completion: every wait for a stage is
+  // an explicit vmcnt(0) followed by the barrier.  The barrier for tile kt + 1
+  // sits inside the last k-step of tile kt: once every wave has read its last
+  // fragments of stage kt & 1 and the DMA of tile kt + 1 has landed, the first
+  // fragments of tile kt + 1 are read while the last MFMAs of tile kt issue,
+  // and the DMA of tile kt + 2 refills the stage just drained.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (nk > 1) issue(1);
+  read_frags(smem, smem + NA * TILE_A, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    // the compiler does not track LDS-DMA completion: wait explicitly
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (kt + 1 < nk) issue(kt + 1);
     const T* sA = smem + (kt & 1) * STAGE;
     const T* sB = sA + NA * TILE_A;
-    read_frags(sA, sB, 0, 0);
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
       const int cur = ks & 1;
-      if (ks + 1 < KSTEPS) read_frags(sA, sB, ks + 1, cur ^ 1);
+      if (ks + 1 < KSTEPS) {
+        read_frags(sA, sB, ks + 1, cur ^ 1);
+      } else if (kt + 1 < nk) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        const T* nA = smem + ((kt + 1) & 1) * STAGE;
+        read_frags(nA, nA + NA * TILE_A, 0, cur ^ 1);
+        if (kt + 2 < nk) issue(kt + 2);
+      }
 #pragma unroll
       for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
