@@ -52,11 +52,29 @@ struct RowGroups {
 // scalar registers so that the address arithmetic built on them stays scalar.
 MOE_DEV int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Output-tile order.  Workgroup ids are first made contiguous per XCD
+// (xcd_remap); consecutive ids then walk GM row-tiles down a tile column
+// before moving one column right, so the ~32 workgroups resident on one XCD
+// cover about GM A panels and 32 / GM B panels, which its L2 holds, instead of
+// one A panel and 32 B panels.  Returns false for ids past the nM x nN tiles.
+MOE_DEV bool tile_order(int id, int nM, int nN, int& mt, int& nt) {
+  constexpr int GM = 4;
+  const int g = uni(id / (GM * nN));
+  const int r = id - g * (GM * nN);
+  const int gm = min(GM, nM - g * GM);
+  if (gm <= 0) return false;
+  mt = uni(g * GM + r % gm);
+  nt = uni(r / gm);
+  return nt < nN;
+}
+
 MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, int& row0,
                           int& mv, int& n0) {
   const int nN = (N + BN - 1) / BN;
+  const int nM = g.offsets == nullptr ? (g.M + BM - 1) / BM : g.tile_prefix[g.G];
   const int id = xcd_remap(blockIdx.x, gridDim.x);
-  const int mt = uni(id / nN), nt = uni(id % nN);
+  int mt, nt;
+  if (!tile_order(id, nM, nN, mt, nt)) return false;
   n0 = nt * BN;
   if (g.offsets == nullptr) {
     grp = 0;
@@ -64,7 +82,6 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
     mv = min(BM, g.M - row0);
     return mv > 0;
   }
-  if (mt >= g.tile_prefix[g.G]) return false;
   grp = uni(find_group(g.tile_prefix, g.G, mt));
   const int local = (mt - g.tile_prefix[grp]) * BM;
   row0 = uni(g.offsets[grp] + local);
