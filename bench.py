@@ -145,6 +145,47 @@ def cpu_baseline(wl, seconds, threads):
             "kind": "port", "sample": sample, "seconds": round(t, 3)}
 
 
+def achievable_peaks():
+    """Library bf16 GEMMs (hipBLASLt through torch.matmul) at a square shape and
+    at the expert / shared-expert shapes of configs 2 and 5, and a plain 1 GiB
+    device copy: the achievable ceilings the roofline fractions are read
+    against, next to the datasheet peaks."""
+    import torch
+    dev = torch.device("cuda:0")
+    res = {"gemm_bf16_tflops": {}, "peak_bf16_tflops": PEAK_BF16_TFLOPS,
+           "peak_hbm_gbs": PEAK_HBM_GBS}
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    shapes = [(8192, 8192, 8192), (16384, 2816, 2048), (16384, 2048, 1408),
+              (8192, 5632, 2048), (8192, 2048, 2816), (2048, 4096, 7168)]
+    for M, N, K in shapes:
+        a = torch.randn(M, K, device=dev, dtype=torch.bfloat16)
+        b = torch.randn(N, K, device=dev, dtype=torch.bfloat16)
+        for _ in range(3):
+            c = a @ b.t()
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(20):
+            c = a @ b.t()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / 20
+        res["gemm_bf16_tflops"][f"{M}x{N}x{K}"] = round(2 * M * N * K / ms / 1e9, 1)
+        del a, b, c
+    x = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(10):
+        y.copy_(x)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / 10
+    res["copy_1GiB_read_plus_write_gbs"] = round(2 * (1 << 30) / ms / 1e6, 1)
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -155,9 +196,15 @@ def main():
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches) and exit: the "
                          "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
+    ap.add_argument("--achievable-peaks", action="store_true",
+                    help="only measure this box's achievable peaks (library bf16 GEMMs through "
+                         "torch.matmul = hipBLASLt, and a 1 GiB device copy) and exit")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
     args = ap.parse_args()
+    if args.achievable_peaks:
+        achievable_peaks()
+        return
     if args.copy_calibration:
         import torch
         n = args.copy_calibration * (1 << 20) // 4
@@ -219,15 +266,18 @@ def main():
         has_grad = torch.empty(E, dtype=torch.uint8, device=dev)
 
     def step():
-        plan.forward(x, w, out=out, saved=saved, aux=aux, z=z)
         if wl.backward:
+            plan.forward(x, w, out=out, saved=saved, aux=aux, z=z)
             plan.backward(x, dout, w, g, saved, dx=dx, d_aux=d_aux, d_z=d_z, has_grad=has_grad)
+        else:  # forward-only call: no saved state, no gate / up pre-activations
+            plan.forward(x, w, out=out, aux=aux, z=z, need_grad=False)
 
     dominant = "gateup_fwd"
+    plan.forward(x, w, out=out, saved=saved, aux=aux, z=z)  # realized routing (untimed)
+    counts = plan.saved_field(saved, T, "counts").cpu()
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    counts = plan.saved_field(saved, T, "counts").cpu()
     plan.stage_times(reset=True)
     plan.set_profiling([dominant])
     torch.cuda.synchronize()
@@ -262,7 +312,7 @@ def main():
     dom_flops = 4 * TK * H * I
     if not wl.backward:  # small-token forward: HBM bound on the expert weights touched
         b = 2
-        dom_bytes = n_touched * 2 * H * I * b + TK * H * b + 3 * TK * I * b
+        dom_bytes = n_touched * 2 * H * I * b + TK * H * b + TK * I * b
         roof = {"bound": "hbm", "achieved": round(dom_bytes / (dom_avg_ms * 1e-3) / 1e9, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
         roof["frac"] = round(roof["achieved"] / PEAK_HBM_GBS, 4)

@@ -109,7 +109,11 @@ typedef struct {
  * src/model.rs:1878).  Writes out [T, H], and the fp32 scalars *aux_loss and
  * *z_loss (device pointers; MoeOutput::aux_loss / z_loss, src/model.rs:1884).
  * `saved` receives routing and activations for moe_backward; it must stay
- * untouched until then.  Replaces MoeLayer::forward (src/model.rs:1834). */
+ * untouched until then.  saved == NULL makes a forward-only call (the
+ * need_grad = 0 case: eval under no_grad, src/eval/run.rs:74): no state
+ * outlives the call, the routing and activations live in `workspace`, and the
+ * gate / up pre-activations that only a backward reads are not computed into
+ * memory.  Replaces MoeLayer::forward (src/model.rs:1834). */
 moe_status moe_forward(moe_plan* plan, void* stream, int64_t num_tokens, const void* x,
                        const moe_weights* w, void* out, float* aux_loss, float* z_loss,
                        void* saved, void* workspace);

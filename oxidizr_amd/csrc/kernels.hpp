@@ -478,7 +478,8 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 
 // ------------------------------------------------------------------ expert GEMMs (forward)
 // G = X Wg^T, U = X Wu^T, A = silu(G) * U for each row group (expert), or for
-// all T rows (shared expert, groups.offsets == nullptr).
+// all T rows (shared expert, groups.offsets == nullptr).  G and U are written
+// only when G is not null (a forward that keeps state for a backward).
 // GROUPED: expert row groups (offsets set); otherwise one dense group (a
 // separate instantiation, so profiles tell the two launches apart).
 template <typename T, bool GROUPED>
@@ -505,8 +506,10 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
 #pragma unroll
     for (int i = 0; i < 8; ++i) act[i] = silu_f(v[0][i]) * v[1][i];
     const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
-    store8(G + o, v[0]);
-    store8(U + o, v[1]);
+    if (G) {  // pre-activations are kept only for a backward
+      store8(G + o, v[0]);
+      store8(U + o, v[1]);
+    }
     store8(A + o, act);
   });
 }
@@ -867,7 +870,8 @@ __global__ void k_has_grad(const int* __restrict__ counts, int E, uint8_t* __res
 // weight row and of its token row, so the four lanes of a row read 64
 // contiguous bytes per load instruction.  Experts without tokens read
 // no weights.  GATEUP: out0 = G, out1 = U, out2 = silu(G) * U from W0 = W_g,
-// W1 = W_u; otherwise out0 = X W0^T (down projection).
+// W1 = W_u (out0 and out1 skipped when out0 is null); otherwise out0 = X W0^T
+// (down projection).
 constexpr int kSkinnyMaxTokens = 64;
 
 MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b) {
@@ -960,8 +964,10 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
       const int64_t o = (int64_t)(r0 + t) * N + n;
       if constexpr (GATEUP) {
         const float gv = gv4[r], uv = acc[c][r];
-        out0[o] = f2bf(gv);
-        out1[o] = f2bf(uv);
+        if (out0) {  // pre-activations are kept only for a backward
+          out0[o] = f2bf(gv);
+          out1[o] = f2bf(uv);
+        }
         out2[o] = f2bf(silu_f(gv) * uv);
       } else {
         out0[o] = f2bf(acc[c][r]);

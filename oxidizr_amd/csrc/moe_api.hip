@@ -64,7 +64,7 @@ struct SavedLayout {
 
 struct WsLayout {
   // forward
-  size_t block_hist, block_base, colpart, sY;
+  size_t block_hist, block_base, colpart, sY, infer;
   // backward
   size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared;
   size_t total;
@@ -140,7 +140,9 @@ struct moe_plan {
   int E() const { return cfg.num_experts; }
   int es() const { return elt_size(cfg.dtype); }
 
-  SavedLayout saved_layout(int64_t T) const {
+  // train == false: the transient state of a forward-only call, without the
+  // gate / up pre-activations that only a backward reads.
+  SavedLayout saved_layout(int64_t T, bool train = true) const {
     const int E = cfg.num_experts, k = cfg.experts_per_tok, H = cfg.hidden,
               I = cfg.intermediate, S = cfg.shared_intermediate;
     const int64_t TK = T * k;
@@ -160,12 +162,12 @@ struct moe_plan {
     fld(MOE_SAVED_MEAN_PROB, 4 * (size_t)E);
     L.tile_prefix = c.take(4 * (size_t)kNumTileBM * (E + 1));
     fld(MOE_SAVED_X_PERM, b * TK * H);
-    fld(MOE_SAVED_GATE_ACT, b * TK * I);
-    fld(MOE_SAVED_UP_ACT, b * TK * I);
+    fld(MOE_SAVED_GATE_ACT, train ? b * TK * I : 0);
+    fld(MOE_SAVED_UP_ACT, train ? b * TK * I : 0);
     fld(MOE_SAVED_SWIGLU, b * TK * I);
     fld(MOE_SAVED_EXPERT_OUT, b * TK * H);
-    L.sG = c.take(b * T * S);
-    L.sU = c.take(b * T * S);
+    L.sG = c.take(train ? b * T * S : 0);
+    L.sU = c.take(train ? b * T * S : 0);
     L.sA = c.take(b * T * S);
     L.total = c.off;
     return L;
@@ -183,6 +185,9 @@ struct moe_plan {
     L.block_base = f.take(4 * (size_t)nb * E);
     L.colpart = f.take(4 * (size_t)nrb * E);
     L.sY = f.take(b * T * H);
+    // forward-only calls keep their routing and activations here, clear of
+    // the forward scratch above (the backward regions below are unused then)
+    L.infer = f.take(saved_layout(T, false).total);
     Carve g;
     g.take(4 * (size_t)nrb * E);  // column partials of the router-bias gradient (offset 0)
     L.dw = g.take(4 * TK);
@@ -370,8 +375,12 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
             I = c.intermediate, S = c.shared_intermediate;
   const int64_t TK = T64 * k;
-  const SavedLayout L = p->saved_layout(T64);
+  // saved == nullptr: forward only (no backward follows); the state lives in
+  // the workspace and the gate / up pre-activations are not written
+  const bool train = saved != nullptr;
+  const SavedLayout L = p->saved_layout(T64, train);
   const WsLayout W = p->ws_layout(T64);
+  if (!train) saved = ws + W.infer;
   // Shared expert first, on the plan's second stream: it only needs x.
   D* sY = nullptr;
   const bool skinny_sh = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
@@ -382,8 +391,8 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
       HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
     }
     StageTimer st(p, ss, MOE_STAGE_SHARED_FWD);
-    D* sG = (D*)(saved + L.sG);
-    D* sU = (D*)(saved + L.sU);
+    D* sG = train ? (D*)(saved + L.sG) : nullptr;
+    D* sU = train ? (D*)(saved + L.sU) : nullptr;
     D* sA = (D*)(saved + L.sA);
     sY = (D*)(ws + W.sY);
     if (skinny_sh && T <= 16) {
@@ -436,8 +445,8 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
   const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
   D* xp = (D*)(saved + L.f[MOE_SAVED_X_PERM]);
-  D* G = (D*)(saved + L.f[MOE_SAVED_GATE_ACT]);
-  D* U = (D*)(saved + L.f[MOE_SAVED_UP_ACT]);
+  D* G = train ? (D*)(saved + L.f[MOE_SAVED_GATE_ACT]) : nullptr;
+  D* U = train ? (D*)(saved + L.f[MOE_SAVED_UP_ACT]) : nullptr;
   D* A = (D*)(saved + L.f[MOE_SAVED_SWIGLU]);
   D* Y = (D*)(saved + L.f[MOE_SAVED_EXPERT_OUT]);
   {
@@ -796,7 +805,7 @@ moe_status moe_forward(moe_plan* p, void* stream, int64_t T, const void* x, cons
   if ((st = check_tokens(T)) != MOE_OK) return st;
   if (!w) return fail(MOE_ERR_INVALID, "weights struct is NULL");
   const moe_config& c = p->cfg;
-  if (T > 0 && (!x || !out || !saved || !workspace || !w->router || !w->gate || !w->up || !w->down))
+  if (T > 0 && (!x || !out || !workspace || !w->router || !w->gate || !w->up || !w->down))
     return fail(MOE_ERR_INVALID, "a required pointer is NULL");
   if (c.has_router_bias && !w->router_bias)
     return fail(MOE_ERR_INVALID, "has_router_bias is set but router_bias is NULL");

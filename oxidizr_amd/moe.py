@@ -184,11 +184,13 @@ class Plan:
             g.shared_gate, g.shared_up, g.shared_down = (t.data_ptr() for t in shared)
         return g, tabs
 
-    def forward(self, x2d, wstruct, out=None, saved=None, aux=None, z=None):
+    def forward(self, x2d, wstruct, out=None, saved=None, aux=None, z=None, need_grad=True):
+        """need_grad=False: forward-only call (eval under no_grad); no saved
+        state is allocated or returned."""
         T = x2d.shape[0]
         if out is None:
             out = torch.empty_like(x2d)
-        if saved is None:
+        if saved is None and need_grad:
             saved = self.new_saved(T)
         if aux is None:
             aux = torch.empty((), dtype=torch.float32, device=self.device)
@@ -361,6 +363,18 @@ class MoeLayer(torch.nn.Module):
         if self.shared_expert is not None:
             params += [self.shared_expert.gate_proj.weight, self.shared_expert.up_proj.weight,
                        self.shared_expert.down_proj.weight]
+        tracked = [x2d, self.router.gate.weight] + params
+        if self.router.bias is not None:
+            tracked.append(self.router.bias)
+        if not (torch.is_grad_enabled() and any(t.requires_grad for t in tracked)):
+            # no backward can follow: forward-only call, no saved state
+            plan = self.plan(x2d)
+            shared = params[3 * self.num_experts:] if self.shared_expert is not None else None
+            E = self.num_experts
+            w, keep = plan.weights_struct(self.router.gate.weight, params[0:E], params[E:2 * E],
+                                          params[2 * E:3 * E], self.router.bias, shared)
+            out, aux, z, _ = plan.forward(x2d, w, need_grad=False)
+            return out.reshape(B, S, H), aux, z
         out, aux, z = _MoeFunction.apply(self, x2d, self.router.gate.weight, self.router.bias,
                                          *params)
         return out.reshape(B, S, H), aux, z

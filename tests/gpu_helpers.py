@@ -37,8 +37,9 @@ class Case:
 
 
 def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x=None,
-            overlap=True):
-    """Forward (+ backward) on cuda:0. Returns a dict of numpy results."""
+            overlap=True, need_grad=True):
+    """Forward (+ backward) on cuda:0. Returns a dict of numpy results.
+    need_grad=False: forward-only call without saved state (out, aux, z only)."""
     dev = torch.device("cuda:0")
     p = case.p
     dt = case.tdtype
@@ -54,12 +55,13 @@ def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x
     gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
     shared = (t["shared_gate"], t["shared_up"], t["shared_down"]) if case.S else None
     w, _keep = plan.weights_struct(t["router"], gate, up, down, bias, shared)
-    out, aux, z, saved = plan.forward(t["x"], w)
+    out, aux, z, saved = plan.forward(t["x"], w, need_grad=need_grad)
     res = {"out": out, "aux": aux, "z": z}
-    for f in ("logits", "probs", "lse", "topk_idx", "topk_w", "counts", "offsets", "perm",
-              "inv_perm"):
-        res[f] = plan.saved_field(saved, T, f)
-    if backward:
+    if need_grad:
+        for f in ("logits", "probs", "lse", "topk_idx", "topk_w", "counts", "offsets", "perm",
+                  "inv_perm"):
+            res[f] = plan.saved_field(saved, T, f)
+    if backward and need_grad:
         fill = float("nan") if nan_fill else 0.0
         g_router = torch.empty_like(t["router"])
         g_bias = torch.empty_like(bias) if bias is not None else None

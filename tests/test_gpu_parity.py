@@ -14,7 +14,7 @@ import pytest
 import torch
 
 from oracle import moe_oracle as mo
-from oxidizr_amd.moe import MoeConfig, Plan
+from oxidizr_amd.moe import MoeConfig, MoeLayer, Plan
 from oxidizr_amd.synth import zipf_bias
 from tests.gpu_helpers import Case, gpu_run, oracle_run, rel
 
@@ -226,3 +226,30 @@ def test_small_batch_path_agrees_with_tiled_path():
     np.testing.assert_array_equal(full["topk_idx"][:37], sub["topk_idx"])
     assert rel(sub["out"], full["out"][:37]) < 1e-2
     assert rel(sub["dx"], full["dx"][:37]) < 1e-2
+
+
+# ---------------------------------------------------------------- forward only
+
+@pytest.mark.parametrize("dtype,T", [("f32", 300), ("bf16", 300), ("bf16", 40), ("bf16", 9)])
+def test_forward_only_matches_training_forward(dtype, T):
+    # saved == NULL (eval under no_grad, reference src/eval/run.rs:74): the same
+    # kernels without the gate / up pre-activation stores, so the same bits
+    case = Case(T=T, H=128, E=16, k=2, I=64, S=64, dtype=dtype, w_std=0.05, seed=11)
+    a = gpu_run(case, backward=False)
+    b = gpu_run(case, backward=False, need_grad=False)
+    for n in ("out", "aux", "z"):
+        np.testing.assert_array_equal(a[n], b[n], err_msg=n)
+
+
+def test_layer_under_no_grad_matches_grad_path():
+    torch.manual_seed(0)
+    dev = torch.device("cuda:0")
+    cfg = MoeConfig(hidden_size=128, num_experts=8, experts_per_tok=2, intermediate_size=64)
+    layer = MoeLayer(cfg, dtype=torch.bfloat16, device=dev)
+    x = torch.randn(2, 50, 128, device=dev).to(torch.bfloat16)
+    out_g, aux_g, z_g = layer(x)
+    with torch.no_grad():
+        out_n, aux_n, z_n = layer(x)
+    assert out_g.requires_grad and not out_n.requires_grad
+    assert torch.equal(out_g.detach(), out_n)
+    assert torch.equal(aux_g.detach(), aux_n) and torch.equal(z_g.detach(), z_n)
