@@ -567,38 +567,50 @@ MOE_DEV void for_each_frag(const f32x16 (&acc)[NACC][C::TN][C::TM], F&& f) {
 template <class C, int NACC>
 constexpr int epi_lds_floats() { return 4 * NACC * C::WM * 36; }
 
-// Row epilogue: calls f(m_local, n_local, v) with v[x][i] = acc[x] at
+// Row epilogue: calls f(m_local, n_local, v, q) with v[x][i] = acc[x] at
 // (m_local, n_local + i) for i < 8, n_local a multiple of 8.  The accumulators
 // of one 32-column block are first written to a wave-private LDS region and
 // read back as rows, so the caller's element-wise work runs on 8 consecutive
 // outputs per lane (16-byte bf16 stores) and only one block's accumulators is
 // in VGPRs at a time.  The LDS must no longer be in use by the main loop (it
 // ends with a barrier); regions are wave-private, so no barrier is needed.
-template <class C, int NACC, class F>
-MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, F&& f) {
+// With NPRE > 0, pre(m_local, n_local, q) is called for every row of a block
+// before any row of it is visited: it issues the NPRE 16-byte loads the visit
+// needs into q, so a block's loads are all in flight together instead of
+// being waited for row group by row group.
+template <class C, int NACC, int NPRE, class PRE, class F>
+MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, PRE&& pre,
+                               F&& f) {
   static_assert(C::WM % 16 == 0, "rows are visited 16 at a time");
   constexpr int P = 36;  // padded row pitch (floats)
+  constexpr int NQ = NPRE > 0 ? NPRE : 1;
+  constexpr int RG = C::WM / 16;  // row groups of a block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   float* reg = lds + wave * NACC * C::WM * P;
 #pragma unroll
   for (int tn = 0; tn < C::TN; ++tn) {  // unrolled: acc is indexed by constants only
+    u32x4 q[RG][NQ];
+    if constexpr (NPRE > 0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g)
+        pre(wm * C::WM + g * 16 + (lane >> 2), wn * C::WN + tn * 32 + (lane & 3) * 8, q[g]);
+    }
 #pragma unroll
     for (int x = 0; x < NACC; ++x)
 #pragma unroll
       for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int qq = 0; qq < 4; ++qq) {
           const int row = tm * 32 + (lane & 31);
-          const int col = 8 * q + 4 * (lane >> 5);
+          const int col = 8 * qq + 4 * (lane >> 5);
           *reinterpret_cast<f32x4*>(reg + (x * C::WM + row) * P + col) =
-              f32x4{acc[x][tn][tm][4 * q], acc[x][tn][tm][4 * q + 1], acc[x][tn][tm][4 * q + 2],
-                    acc[x][tn][tm][4 * q + 3]};
+              f32x4{acc[x][tn][tm][4 * qq], acc[x][tn][tm][4 * qq + 1],
+                    acc[x][tn][tm][4 * qq + 2], acc[x][tn][tm][4 * qq + 3]};
         }
     __builtin_amdgcn_sched_barrier(0);
-#pragma unroll 2
-    for (int r0 = 0; r0 < C::WM; r0 += 16) {
-      const int row = r0 + (lane >> 2);
+    auto visit = [&](int g) {
+      const int row = g * 16 + (lane >> 2);
       const int col = (lane & 3) * 8;
       float v[NACC][8];
 #pragma unroll
@@ -608,10 +620,23 @@ MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, 
         v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
         v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
       }
-      f(wm * C::WM + row, wn * C::WN + tn * 32 + col, v);
+      f(wm * C::WM + row, wn * C::WN + tn * 32 + col, v, q[g]);
+    };
+    if constexpr (NPRE > 0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g) visit(g);  // q[g] needs constant indices
+    } else {
+#pragma unroll 2
+      for (int g = 0; g < RG; ++g) visit(g);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+template <class C, int NACC, class F>
+MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, F&& f) {
+  for_each_row8_pre<C, NACC, 0>(acc, lds, [](int, int, u32x4*) {},
+                                [&](int m, int n, auto& v, const u32x4*) { f(m, n, v); });
 }
 
 // Store / load 8 consecutive elements (8-element aligned) of one row in global

@@ -44,7 +44,7 @@ struct RowGroups {
   const int* offsets;      // [G + 1] row offsets
   const int* tile_prefix;  // [G + 1] prefix of ceil(count / BM)
   int G;
-  int M;
+  int M;                   // rows in all groups (the extent of row-major operands)
 };
 
 // Tile coordinates are workgroup-uniform, but integer division by a runtime
@@ -637,12 +637,30 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
   zero_acc<C, 1>(acc);
   mainloop<C, T, false, true, 1, 1>(acc, a, b, H, smem);
   static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+  // G and U of a whole 32-column block are requested before its rows are
+  // visited; rows outside the tile read zeros (out-of-range offsets)
+  constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
+  const rsrc_t rg = make_rsrc(G, (uint32_t)((int64_t)groups.M * N * sizeof(T)));
+  const rsrc_t ru = make_rsrc(U, (uint32_t)((int64_t)groups.M * N * sizeof(T)));
+  auto pre = [&](int m, int n, u32x4 (&q)[2 * NV]) {
+    const bool in = m < mv && n0 + n < N;
+    const uint32_t off = in ? (uint32_t)(((int64_t)(row0 + m) * N + n0 + n) * sizeof(T)) : kOobOffset;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      q[j] = buf_ld16(rg, off + 16 * j, 0);
+      q[NV + j] = buf_ld16(ru, off + 16 * j, 0);
+    }
+  };
+  for_each_row8_pre<C, 1, 2 * NV>(acc, reinterpret_cast<float*>(smem), pre,
+                                  [&](int m, int n, auto& v, const u32x4 (&q)[2 * NV]) {
     if (m >= mv || n0 + n >= N) return;
     const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
     float g[8], u[8], dg[8], du[8];
-    load8(G + o, g);
-    load8(U + o, u);
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      unpack16(q[j], g + j * (8 / NV), T());
+      unpack16(q[NV + j], u + j * (8 / NV), T());
+    }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float da = alpha * v[0][i];

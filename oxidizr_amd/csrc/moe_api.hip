@@ -457,7 +457,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const D* const* tg = (const D* const*)p->d_tab;
   const D* const* tu = (const D* const*)(p->d_tab + E);
   const D* const* td = (const D* const*)(p->d_tab + 2 * E);
-  const RowGroups rg{offsets, tprefix, E, 0};
+  const RowGroups rg{offsets, tprefix, E, (int)TK};
   const int mtiles_max = ceil_div(TK, CB::BM) + E;
   // few tokens: no expert holds more than T rows, stream the weights instead
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
@@ -567,7 +567,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdg = (D* const*)(p->d_tab + 3 * E);
   D* const* tdu = (D* const*)(p->d_tab + 4 * E);
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
-  const RowGroups rg{offsets, tprefix, E, 0};
+  const RowGroups rg{offsets, tprefix, E, (int)TK};
   const KGroups kg{offsets, E, 0, 1, 0};
   float* partial = (float*)(ws + W.splitk_router);
   const int mtiles_max = ceil_div(TK, CB::BM) + E;
