@@ -346,66 +346,66 @@ MOE_DEV int wave_incl_scan(int v) {
   return v;
 }
 
-// One block of 256 threads (E <= 1024).  Counts and per-block bases come from
-// the block histograms; the expert counts are then held in LDS and scanned in
-// parallel (each thread owns E/256 consecutive experts) for the offsets and
-// for the tile prefix of every height in kTileBM.  Integer arithmetic only.
-__global__ __launch_bounds__(256) void k_scan(const int* __restrict__ block_hist, int nb, int E,
-                                              int* __restrict__ block_base,
-                                              int* __restrict__ counts,
-                                              int* __restrict__ offsets,
-                                              int* __restrict__ tile_prefix) {
-  __shared__ int cnt[1024], offs[1024];
-  __shared__ int wsum[4];
+// One block of 1024 threads (E <= 1024).  Thread (g, e) = (tid / E, tid % E)
+// owns expert e's histogram entries of a contiguous chunk of blocks: the
+// chunk sums and their exclusive prefix over g give the expert counts and the
+// chunk bases; the expert counts are then scanned in parallel (one expert per
+// thread) for the offsets and for the tile prefix of every height in kTileBM;
+// a last pass writes every block's base.  Integer arithmetic only.
+__global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_hist, int nb, int E,
+                                               int* __restrict__ block_base,
+                                               int* __restrict__ counts,
+                                               int* __restrict__ offsets,
+                                               int* __restrict__ tile_prefix) {
+  __shared__ int cnt[1024], offs[1024], part[1024];
+  __shared__ int wsum[16];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E; e += 256) {
+  const int G = 1024 / E;            // threads per expert
+  const int e = tid % E, g = tid / E;
+  const bool act = g < G;
+  const int chunk = (nb + G - 1) / G;
+  const int b0 = act ? g * chunk : 0, b1 = act ? min(nb, b0 + chunk) : 0;
+  int sum = 0;
+  for (int b = b0; b < b1; ++b) sum += block_hist[(int64_t)b * E + e];
+  part[tid] = sum;
+  __syncthreads();
+  if (tid < E) {
     int run = 0;
-    for (int b = 0; b < nb; ++b) {
-      const int c = block_hist[(int64_t)b * E + e];
-      block_base[(int64_t)b * E + e] = run;
-      run += c;
+    for (int q = 0; q < G; ++q) {
+      const int v = part[q * E + tid];
+      part[q * E + tid] = run;
+      run += v;
     }
-    cnt[e] = run;
-    counts[e] = run;
+    cnt[tid] = run;
+    counts[tid] = run;
   }
   __syncthreads();
-  const int per = (E + 255) / 256;  // <= 4
-  const int e0 = tid * per;
   for (int j = 0; j <= kNumTileBM; ++j) {
     const int bm = j == 0 ? 1 : kTileBM[j - 1];
-    int v[4], tot = 0;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = e0 + i;
-      int c = (i < per && e < E) ? cnt[e] : 0;
-      c = (c + bm - 1) / bm;
-      v[i] = c;
-      tot += c;
-    }
-    const int incl = wave_incl_scan(tot);
+    const int v = tid < E ? (cnt[tid] + bm - 1) / bm : 0;
+    const int incl = wave_incl_scan(v);
     if (lane == 63) wsum[wave] = incl;
     __syncthreads();
     int base = 0;
     for (int w = 0; w < wave; ++w) base += wsum[w];
-    int run = base + incl - tot;
     int* dst = j == 0 ? offsets : tile_prefix + (j - 1) * (E + 1);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int e = e0 + i;
-      if (i < per && e < E) {
-        dst[e] = run;
-        if (j == 0) offs[e] = run;
-        run += v[i];
-      }
+    if (tid < E) {
+      dst[tid] = base + incl - v;
+      if (j == 0) offs[tid] = base + incl - v;
     }
-    if (tid == 255) dst[E] = base + incl;
+    if (tid == 1023) dst[E] = base + incl;
     __syncthreads();
   }
-  for (int e = tid; e < E; e += 256) {
-    const int base = offs[e];
-    for (int b = 0; b < nb; ++b) block_base[(int64_t)b * E + e] += base;
+  if (act) {
+    int run = offs[e] + part[tid];
+    for (int b = b0; b < b1; ++b) {
+      const int c = block_hist[(int64_t)b * E + e];
+      block_base[(int64_t)b * E + e] = run;
+      run += c;
+    }
   }
 }
+
 
 // Stable scatter: position of assignment (t, j) = offset of its expert +
 // number of earlier tokens (same expert) before it.  Ranks inside a wave come
@@ -857,15 +857,36 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
     float r[8], q[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) r[i] = v[0][i];
-    for (int j = 0; j < k; ++j) {
-      int64_t p = inv_perm[(int64_t)t * k + j];
-      p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
-      load8(dXp + p * H + n0 + n, q);
+    // every gathered row is requested before the first one is added (k <= 16,
+    // summed in slot order)
+    constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
+    u32x4 raw[16][NV];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) r[i] += q[i];
+    for (int j = 0; j < 16; ++j) {
+      if (j < k) {
+        int64_t p = inv_perm[(int64_t)t * k + j];
+        p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+#pragma unroll
+        for (int h = 0; h < NV; ++h) raw[j][h] = *gptr(reinterpret_cast<const u32x4*>(dXp + p * H + n0 + n + h * (8 / NV)));
+      }
+    }
+    u32x4 rs[NV];
+    if (dxs) {
+#pragma unroll
+      for (int h = 0; h < NV; ++h) rs[h] = *gptr(reinterpret_cast<const u32x4*>(dxs + (int64_t)t * H + n0 + n + h * (8 / NV)));
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      if (j < k) {
+#pragma unroll
+        for (int h = 0; h < NV; ++h) unpack16(raw[j][h], q + h * (8 / NV), T());
+#pragma unroll
+        for (int i = 0; i < 8; ++i) r[i] += q[i];
+      }
     }
     if (dxs) {
-      load8(dxs + (int64_t)t * H + n0 + n, q);
+#pragma unroll
+      for (int h = 0; h < NV; ++h) unpack16(rs[h], q + h * (8 / NV), T());
 #pragma unroll
       for (int i = 0; i < 8; ++i) r[i] += q[i];
     }

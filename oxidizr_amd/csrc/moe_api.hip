@@ -327,7 +327,7 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
     int* bh = (int*)(ws + W.block_hist);
     int* bb = (int*)(ws + W.block_base);
     hipLaunchKernelGGL(k_hist, dim3(nb), dim3(256), sizeof(int) * E, s, idx, T, k, E, bh);
-    hipLaunchKernelGGL(k_scan, dim3(1), dim3(256), 0, s, bh, nb, E, bb, counts, offsets, tprefix);
+    hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bh, nb, E, bb, counts, offsets, tprefix);
     int nbits = 0;
     while ((1 << nbits) <= E) ++nbits;
     hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), sizeof(int) * 8 * E, s, idx, T, k, E,
