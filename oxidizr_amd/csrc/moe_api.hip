@@ -74,20 +74,33 @@ int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 int round8(int v) { return (v + 7) / 8 * 8; }
 
-// Split of a dense (all-token) weight gradient over K = tokens: enough fixed
-// chunks for about two rounds of workgroups on 256 CUs, each chunk at least
-// four k-tiles.  The split depends only on the shapes, never on timing.
+// Split of a dense (all-token) weight gradient over K = tokens into fixed
+// chunks (each at least four k-tiles).  The count minimises a cost model in
+// units of one workgroup k-tile: rounds of workgroups on 256 CUs times k-tiles
+// per chunk, plus, when split, the fp32 partial tiles written and read back by
+// k_splitk_reduce (8 bytes per output element and chunk at ~5 TB/s, against
+// ~3.9 TFLOP/s of MFMA work per CU: 3.1 * M * N / (BM * BN * BK) units per
+// chunk).  The split depends only on the shapes, never on timing.
 struct SplitPlan {
   int nsplit, kchunk;
 };
 template <class C>
 SplitPlan plan_split(int M, int N, int K) {
   const int tiles = ceil_div(M, C::BM) * ceil_div(N, C::BN);
-  const int want = ceil_div(512, tiles);
+  const int nkt = ceil_div(K, C::BK);
   const int most = K / (4 * C::BK) > 1 ? K / (4 * C::BK) : 1;
-  int ns = want < most ? want : most;
-  if (ns < 1) ns = 1;
-  const int chunk = ceil_div(ceil_div(K, ns), C::BK) * C::BK;
+  const double red = 3.1 * (double)M * N / ((double)C::BM * C::BN * C::BK);
+  int best = 1;
+  double best_cost = 0;
+  for (int ns = 1; ns <= most && ns <= 64; ++ns) {
+    const double cost = (double)ceil_div((int64_t)tiles * ns, 256) * ceil_div(nkt, ns) +
+                        (ns > 1 ? red * ns : 0.0);
+    if (ns == 1 || cost < best_cost) {
+      best = ns;
+      best_cost = cost;
+    }
+  }
+  const int chunk = ceil_div(ceil_div(K, best), C::BK) * C::BK;
   return {ceil_div(K, chunk), chunk};
 }
 
