@@ -201,6 +201,10 @@ def main():
                          "torch.matmul = hipBLASLt, and a 1 GiB device copy) and exit")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--recompute", action="store_true",
+                    help="keep only the routing state between forward and backward and "
+                         "recompute the expert activations in the backward (the plan's "
+                         "recompute_activations; activation checkpointing)")
     args = ap.parse_args()
     if args.achievable_peaks:
         achievable_peaks()
@@ -246,7 +250,8 @@ def main():
 
     cfg = MoeConfig(hidden_size=H, num_experts=E, experts_per_tok=k, intermediate_size=I,
                     shared_expert_enabled=S > 0, shared_intermediate_size=S or None,
-                    load_balance_alpha=wl.alpha, router_bias=bias is not None)
+                    load_balance_alpha=wl.alpha, router_bias=bias is not None,
+                    recompute_activations=bool(args.recompute))
     plan = Plan(cfg, dtype, dev)
     w, _keep_w = plan.weights_struct(router, list(gate.unbind(0)), list(up.unbind(0)),
                                      list(down.unbind(0)), bias, shared)
@@ -352,7 +357,10 @@ def main():
                    "experts_per_tok": k, "intermediate": I, "shared_intermediate": S,
                    "load_balance_alpha": wl.alpha, "pass": "fwd+bwd" if wl.backward else "fwd",
                    "parallelism": "single GPU", "routing": wl.skew, **skew_info,
-                   "max_expert_tokens": int(counts.max()), "empty_experts": int((counts == 0).sum())},
+                   "max_expert_tokens": int(counts.max()), "empty_experts": int((counts == 0).sum()),
+                   "activations": "recomputed in backward" if args.recompute else "kept",
+                   "saved_MB_per_layer": round(plan.saved_bytes(T) / 1e6, 1),
+                   "workspace_MB": round(plan.workspace_bytes(T) / 1e6, 1)},
         "roofline": roof,
         "layer_tflops": round(total_flops / (elapsed / args.steps) / 1e12, 1),
         "layer_mfma_frac": round(total_flops / (elapsed / args.steps) / 1e12 / peak, 4),

@@ -64,10 +64,15 @@ typedef struct {
   float shared_expert_scale;    /* s: out += s * shared(x) (src/model.rs:1923)     */
   float aux_switch_coef;        /* aux = E*(c_sw*sum_e f_e P_e + c_sq*sum_e P_e^2)  */
   float aux_sqprob_coef;        /*   (SwitchPlusSquaredProb, src/model.rs:1905)     */
+  int32_t recompute_activations;/* 1: `saved` keeps the routing state only and
+                                   moe_backward recomputes the expert activations
+                                   first (trainer.activation_checkpointing covering
+                                   this layer, src/config/activation_checkpointing.rs
+                                   :25-35, src/model/recompute/segment.rs:58-170)  */
 } moe_config;
 
 /* Fills cfg with the documented defaults: tau = 1, s = 1, c_sw = c_sq = 1,
- * no renormalisation, no router bias, bf16. */
+ * no renormalisation, no router bias, bf16, activations kept. */
 void moe_config_default(moe_config* cfg, int32_t hidden, int32_t num_experts,
                         int32_t experts_per_tok, int32_t intermediate,
                         int32_t shared_intermediate);
@@ -168,7 +173,7 @@ typedef enum {
   MOE_STAGE_GATEUP_FWD, MOE_STAGE_DOWN_FWD, MOE_STAGE_SHARED_FWD, MOE_STAGE_COMBINE_FWD,
   MOE_STAGE_LOSSES, MOE_STAGE_COMBINE_BWD, MOE_STAGE_DOWN_DGRAD, MOE_STAGE_DOWN_WGRAD,
   MOE_STAGE_GATEUP_DGRAD, MOE_STAGE_GATEUP_WGRAD, MOE_STAGE_SHARED_BWD, MOE_STAGE_ROUTER_BWD,
-  MOE_STAGE_DX, MOE_NUM_STAGES
+  MOE_STAGE_DX, MOE_STAGE_RECOMPUTE, MOE_NUM_STAGES
 } moe_stage;
 const char* moe_stage_name(int32_t stage);
 moe_status moe_plan_set_profiling(moe_plan* plan, int32_t stage_mask);

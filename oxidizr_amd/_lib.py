@@ -22,7 +22,7 @@ EXPORTED = [
     "moe_plan_set_shared_overlap",
     "moe_last_error", "moe_version",
 ]
-NUM_STAGES = 17
+NUM_STAGES = 18
 
 
 class MoeConfigC(ctypes.Structure):
@@ -33,6 +33,7 @@ class MoeConfigC(ctypes.Structure):
         ("norm_topk_prob", ctypes.c_int32), ("has_router_bias", ctypes.c_int32),
         ("router_temperature", ctypes.c_float), ("shared_expert_scale", ctypes.c_float),
         ("aux_switch_coef", ctypes.c_float), ("aux_sqprob_coef", ctypes.c_float),
+        ("recompute_activations", ctypes.c_int32),
     ]
 
 

@@ -59,6 +59,7 @@ struct SavedLayout {
   size_t f[MOE_SAVED_NUM_FIELDS];
   size_t fbytes[MOE_SAVED_NUM_FIELDS];
   size_t tile_prefix, sG, sU, sA;
+  size_t sGbytes, sUbytes, sAbytes;
   size_t total;
 };
 
@@ -66,7 +67,8 @@ struct WsLayout {
   // forward
   size_t block_hist, block_base, colpart, sY, infer;
   // backward
-  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared;
+  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
+      recomp;
   size_t total;
 };
 
@@ -153,9 +155,13 @@ struct moe_plan {
   int E() const { return cfg.num_experts; }
   int es() const { return elt_size(cfg.dtype); }
 
-  // train == false: the transient state of a forward-only call, without the
-  // gate / up pre-activations that only a backward reads.
-  SavedLayout saved_layout(int64_t T, bool train = true) const {
+  // Which state a layout holds.  All: routing and every activation (the
+  // default `saved`, and the activations a recomputing backward rebuilds);
+  // Transient: the state of a forward that no backward reads (no gate / up
+  // pre-activations); Routing: the routing state alone (the `saved` of a plan
+  // with recompute_activations).
+  enum class Keep { All, Transient, Routing };
+  SavedLayout saved_layout(int64_t T, Keep keep) const {
     const int E = cfg.num_experts, k = cfg.experts_per_tok, H = cfg.hidden,
               I = cfg.intermediate, S = cfg.shared_intermediate;
     const int64_t TK = T * k;
@@ -174,16 +180,24 @@ struct moe_plan {
     fld(MOE_SAVED_INV_PERM, 4 * TK);
     fld(MOE_SAVED_MEAN_PROB, 4 * (size_t)E);
     L.tile_prefix = c.take(4 * (size_t)kNumTileBM * (E + 1));
-    fld(MOE_SAVED_X_PERM, b * TK * H);
-    fld(MOE_SAVED_GATE_ACT, train ? b * TK * I : 0);
-    fld(MOE_SAVED_UP_ACT, train ? b * TK * I : 0);
-    fld(MOE_SAVED_SWIGLU, b * TK * I);
-    fld(MOE_SAVED_EXPERT_OUT, b * TK * H);
-    L.sG = c.take(train ? b * T * S : 0);
-    L.sU = c.take(train ? b * T * S : 0);
-    L.sA = c.take(b * T * S);
+    const bool act = keep != Keep::Routing, pre = keep == Keep::All;
+    fld(MOE_SAVED_X_PERM, act ? b * TK * H : 0);
+    fld(MOE_SAVED_GATE_ACT, pre ? b * TK * I : 0);
+    fld(MOE_SAVED_UP_ACT, pre ? b * TK * I : 0);
+    fld(MOE_SAVED_SWIGLU, act ? b * TK * I : 0);
+    fld(MOE_SAVED_EXPERT_OUT, act ? b * TK * H : 0);
+    L.sGbytes = L.sUbytes = pre ? b * T * S : 0;
+    L.sAbytes = act ? b * T * S : 0;
+    L.sG = c.take(L.sGbytes);
+    L.sU = c.take(L.sUbytes);
+    L.sA = c.take(L.sAbytes);
     L.total = c.off;
     return L;
+  }
+
+  // layout of the caller's `saved` buffer
+  SavedLayout kept_layout(int64_t T) const {
+    return saved_layout(T, cfg.recompute_activations ? Keep::Routing : Keep::All);
   }
 
   WsLayout ws_layout(int64_t T) const {
@@ -200,7 +214,7 @@ struct moe_plan {
     L.sY = f.take(b * T * H);
     // forward-only calls keep their routing and activations here, clear of
     // the forward scratch above (the backward regions below are unused then)
-    L.infer = f.take(saved_layout(T, false).total);
+    L.infer = f.take(saved_layout(T, Keep::Transient).total);
     Carve g;
     g.take(4 * (size_t)nrb * E);  // column partials of the router-bias gradient (offset 0)
     L.dw = g.take(4 * TK);
@@ -218,6 +232,8 @@ struct moe_plan {
                                  : splitk_bytes<bf16_t>(cfg, T, false));
     L.splitk_shared = g.take(f32 ? splitk_bytes<float>(cfg, T, true)
                                  : splitk_bytes<bf16_t>(cfg, T, true));
+    // a recomputing backward rebuilds every activation here first
+    L.recomp = g.take(cfg.recompute_activations ? saved_layout(T, Keep::All).total : 0);
     L.total = f.off > g.off ? f.off : g.off;
     return L;
   }
@@ -376,6 +392,143 @@ void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, co
   }
 }
 
+// Pointers to the routing state and the activations of one call.  The
+// routing state lives in `saved` (or, for a forward-only call, the
+// workspace); the activations live in `saved` unless the plan recomputes
+// them (forward: transient workspace region; backward: rebuilt in the
+// workspace before use).  G, U, sG, sU are null where they are not kept.
+template <typename D>
+struct State {
+  float *logits, *probs, *lse, *w, *P;
+  int *idx, *counts, *offsets, *perm, *inv, *tprefix;
+  D *xp, *G, *U, *A, *Y, *sG, *sU, *sA;
+  State(char* rb, const SavedLayout& LR, char* ab, const SavedLayout& LA) {
+    auto r = [&](int f) { return rb + LR.f[f]; };
+    auto a = [&](int f) { return LA.fbytes[f] ? (D*)(ab + LA.f[f]) : nullptr; };
+    logits = (float*)r(MOE_SAVED_LOGITS);
+    probs = (float*)r(MOE_SAVED_PROBS);
+    lse = (float*)r(MOE_SAVED_LSE);
+    idx = (int*)r(MOE_SAVED_TOPK_IDX);
+    w = (float*)r(MOE_SAVED_TOPK_W);
+    counts = (int*)r(MOE_SAVED_COUNTS);
+    offsets = (int*)r(MOE_SAVED_OFFSETS);
+    perm = (int*)r(MOE_SAVED_PERM);
+    inv = (int*)r(MOE_SAVED_INV_PERM);
+    P = (float*)r(MOE_SAVED_MEAN_PROB);
+    tprefix = (int*)(rb + LR.tile_prefix);
+    xp = a(MOE_SAVED_X_PERM);
+    G = a(MOE_SAVED_GATE_ACT);
+    U = a(MOE_SAVED_UP_ACT);
+    A = a(MOE_SAVED_SWIGLU);
+    Y = a(MOE_SAVED_EXPERT_OUT);
+    sG = LA.sGbytes ? (D*)(ab + LA.sG) : nullptr;
+    sU = LA.sUbytes ? (D*)(ab + LA.sU) : nullptr;
+    sA = LA.sAbytes ? (D*)(ab + LA.sA) : nullptr;
+  }
+};
+
+// Shared expert forward over all T tokens on stream ss: G, U (when kept), A,
+// and the down projection into sY when sY is not null.
+template <typename D>
+void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weights* w, D* sG,
+                D* sU, D* sA, D* sY) {
+  using CG = typename Tilings<D>::GateUp;
+  using CB = typename Tilings<D>::Big;
+  const int H = p->cfg.hidden, S = p->cfg.shared_intermediate;
+  const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
+  if (skinny && T <= 16) {
+    hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
+                       (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
+                       nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
+                       (bf16_t*)sA);
+    if (sY)
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
+                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
+                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
+  } else if (skinny) {
+    hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
+                       (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
+                       nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
+                       (bf16_t*)sA);
+    if (sY)
+      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
+                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
+                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
+  } else {
+    const RowGroups dense{nullptr, nullptr, 1, T};
+    hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
+                       dim3(256), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                       (const D*)w->shared_up, H, S, sG, sU, sA);
+    if (sY)
+      hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
+                         dim3(256), 0, ss, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+  }
+}
+
+// Routed experts forward on stream s: gather X_perm, then G, U (when kept),
+// A and the per-assignment expert outputs Y.  `timed`: record the stages.
+template <typename D>
+moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State<D>& st,
+                      bool timed) {
+  using CG = typename Tilings<D>::GateUp;
+  using CB = typename Tilings<D>::Big;
+  const moe_config& c = p->cfg;
+  const int H = c.hidden, E = c.num_experts, k = c.experts_per_tok, I = c.intermediate;
+  const int64_t TK = (int64_t)T * k;
+  const int* tprefix = st.tprefix + tile_slot(CB::BM) * (E + 1);
+  auto stage = [&](int id) { return timed ? id : MOE_STAGE_RECOMPUTE; };
+  {
+    StageTimer tm(p, s, stage(MOE_STAGE_GATHER));
+    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(TK, 4)), dim3(256), 0, s, x, st.perm, T, k, H,
+                       st.xp);
+    LAUNCH_CHECK();
+  }
+  const D* const* tg = (const D* const*)p->d_tab;
+  const D* const* tu = (const D* const*)(p->d_tab + E);
+  const D* const* td = (const D* const*)(p->d_tab + 2 * E);
+  const RowGroups rg{st.offsets, tprefix, E, (int)TK};
+  const int mtiles_max = ceil_div(TK, CB::BM) + E;
+  // few tokens: no expert holds more than T rows, stream the weights instead
+  const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
+  {
+    StageTimer tm(p, s, stage(MOE_STAGE_GATEUP_FWD));
+    if (skinny) {
+      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
+                         (const bf16_t*)st.xp, st.offsets, 0, (const bf16_t* const*)tg, nullptr,
+                         (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G, (bf16_t*)st.U,
+                         (bf16_t*)st.A);
+      if (T > 16)
+        hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
+                           (const bf16_t*)st.xp, st.offsets, 0, (const bf16_t* const*)tg,
+                           nullptr, (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G,
+                           (bf16_t*)st.U, (bf16_t*)st.A);
+    } else {
+      const int grid = mtiles_max * ceil_div(I, CG::BN);
+      hipLaunchKernelGGL((k_gateup_fwd<D, true>), dim3(grid), dim3(256), 0, s, st.xp, rg, tg,
+                         nullptr, tu, nullptr, H, I, st.G, st.U, st.A);
+    }
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer tm(p, s, stage(MOE_STAGE_DOWN_FWD));
+    if (skinny) {
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, 64)), dim3(256), 0, s,
+                         (const bf16_t*)st.A, st.offsets, 0, (const bf16_t* const*)td, nullptr,
+                         nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
+      if (T > 16)
+        hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(E * ceil_div(H, 64)), dim3(256), 0,
+                           s, (const bf16_t*)st.A, st.offsets, 0, (const bf16_t* const*)td,
+                           nullptr, nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
+    } else {
+      const int grid = mtiles_max * ceil_div(H, CB::BN);
+      hipLaunchKernelGGL((k_down_fwd<D, true>), dim3(grid), dim3(256), 0, s, st.A, rg, td,
+                         nullptr, I, H, st.Y);
+    }
+    LAUNCH_CHECK();
+  }
+  return MOE_OK;
+}
+
 template <typename D>
 moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                         const moe_weights* w, D* out, float* aux, float* z, char* saved,
@@ -386,143 +539,61 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   static_assert(CG::BM == CB::BM, "row-grouped GEMMs share one tile-prefix table");
   const moe_config& c = p->cfg;
   const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
-            I = c.intermediate, S = c.shared_intermediate;
-  const int64_t TK = T64 * k;
-  // saved == nullptr: forward only (no backward follows); the state lives in
-  // the workspace and the gate / up pre-activations are not written
+            S = c.shared_intermediate;
+  using Keep = moe_plan::Keep;
+  // saved == nullptr: forward only (no backward follows): the state lives in
+  // the workspace and the gate / up pre-activations are not written.  A plan
+  // with recompute_activations keeps only the routing state in `saved`; the
+  // activations of this call are transient, in the same workspace region.
   const bool train = saved != nullptr;
-  const SavedLayout L = p->saved_layout(T64, train);
+  const bool keep_act = train && !c.recompute_activations;
   const WsLayout W = p->ws_layout(T64);
-  if (!train) saved = ws + W.infer;
+  const SavedLayout LT = p->saved_layout(T64, Keep::Transient);
+  const SavedLayout LR = train ? p->kept_layout(T64) : LT;
+  char* rb = train ? saved : ws + W.infer;
+  char* ab = keep_act ? saved : ws + W.infer;
+  const State<D> st(rb, LR, ab, keep_act ? LR : LT);
   // Shared expert first, on the plan's second stream: it only needs x.
   D* sY = nullptr;
-  const bool skinny_sh = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   if (S > 0) {
     const hipStream_t ss = p->shared_stream(s);
     if (ss != s) {
       HIP_TRY(hipEventRecord(p->fork, s));
       HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
     }
-    StageTimer st(p, ss, MOE_STAGE_SHARED_FWD);
-    D* sG = train ? (D*)(saved + L.sG) : nullptr;
-    D* sU = train ? (D*)(saved + L.sU) : nullptr;
-    D* sA = (D*)(saved + L.sA);
+    StageTimer tm(p, ss, MOE_STAGE_SHARED_FWD);
     sY = (D*)(ws + W.sY);
-    if (skinny_sh && T <= 16) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
-                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
-                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
-                         (bf16_t*)sA);
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
-                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
-                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
-    } else if (skinny_sh) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
-                         (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
-                         nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
-                         (bf16_t*)sA);
-      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
-                         (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
-                         nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
-    } else {
-      const RowGroups dense{nullptr, nullptr, 1, T};
-      hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
-                         dim3(256), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                         (const D*)w->shared_up, H, S, sG, sU, sA);
-      hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
-                         dim3(256), 0, ss, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
-    }
+    shared_fwd<D>(p, ss, T, x, w, st.sG, st.sU, st.sA, sY);
     LAUNCH_CHECK();
     if (ss != s) HIP_TRY(hipEventRecord(p->join, ss));
   }
-  float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
   {
-    StageTimer st(p, s, MOE_STAGE_ROUTER_GEMM);
+    StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
     if (std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens) {
       hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16)), dim3(256), 0, s, (const bf16_t*)x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
-                         logits, T, H, E);
+                         st.logits, T, H, E);
     } else {
       const int grid = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
       hipLaunchKernelGGL(k_router_logits<D>, dim3(grid), dim3(256), 0, s, x, (const D*)w->router,
-                         c.has_router_bias ? w->router_bias : nullptr, logits, T, H, E);
+                         c.has_router_bias ? w->router_bias : nullptr, st.logits, T, H, E);
     }
     LAUNCH_CHECK();
   }
-  moe_status r = run_routing<D>(p, s, T64, saved, ws, L, W);
+  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W);
   if (r != MOE_OK) return r;
-  const int* counts = (const int*)(saved + L.f[MOE_SAVED_COUNTS]);
-  const int* offsets = (const int*)(saved + L.f[MOE_SAVED_OFFSETS]);
-  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(CB::BM) * (E + 1);
-  const int* perm = (const int*)(saved + L.f[MOE_SAVED_PERM]);
-  const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
-  const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
-  D* xp = (D*)(saved + L.f[MOE_SAVED_X_PERM]);
-  D* G = train ? (D*)(saved + L.f[MOE_SAVED_GATE_ACT]) : nullptr;
-  D* U = train ? (D*)(saved + L.f[MOE_SAVED_UP_ACT]) : nullptr;
-  D* A = (D*)(saved + L.f[MOE_SAVED_SWIGLU]);
-  D* Y = (D*)(saved + L.f[MOE_SAVED_EXPERT_OUT]);
-  {
-    StageTimer st(p, s, MOE_STAGE_GATHER);
-    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(TK, 4)), dim3(256), 0, s, x, perm, T, k, H, xp);
-    LAUNCH_CHECK();
-  }
-  const D* const* tg = (const D* const*)p->d_tab;
-  const D* const* tu = (const D* const*)(p->d_tab + E);
-  const D* const* td = (const D* const*)(p->d_tab + 2 * E);
-  const RowGroups rg{offsets, tprefix, E, (int)TK};
-  const int mtiles_max = ceil_div(TK, CB::BM) + E;
-  // few tokens: no expert holds more than T rows, stream the weights instead
-  const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
-  {
-    StageTimer st(p, s, MOE_STAGE_GATEUP_FWD);
-    if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
-                         (const bf16_t*)xp, offsets, 0, (const bf16_t* const*)tg, nullptr,
-                         (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)G, (bf16_t*)U,
-                         (bf16_t*)A);
-      if (T > 16)
-        hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
-                           (const bf16_t*)xp, offsets, 0, (const bf16_t* const*)tg, nullptr,
-                           (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)G, (bf16_t*)U,
-                           (bf16_t*)A);
-    } else {
-      const int grid = mtiles_max * ceil_div(I, CG::BN);
-      hipLaunchKernelGGL((k_gateup_fwd<D, true>), dim3(grid), dim3(256), 0, s, xp, rg, tg, nullptr,
-                         tu, nullptr, H, I, G, U, A);
-    }
-    LAUNCH_CHECK();
-  }
-  {
-    StageTimer st(p, s, MOE_STAGE_DOWN_FWD);
-    if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, 64)), dim3(256), 0, s,
-                         (const bf16_t*)A, offsets, 0, (const bf16_t* const*)td, nullptr, nullptr,
-                         nullptr, I, H, (bf16_t*)Y, nullptr, nullptr);
-      if (T > 16)
-        hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(E * ceil_div(H, 64)), dim3(256), 0,
-                           s, (const bf16_t*)A, offsets, 0, (const bf16_t* const*)td, nullptr,
-                           nullptr, nullptr, I, H, (bf16_t*)Y, nullptr, nullptr);
-    } else {
-      const int grid = mtiles_max * ceil_div(H, CB::BN);
-      hipLaunchKernelGGL((k_down_fwd<D, true>), dim3(grid), dim3(256), 0, s, A, rg, td, nullptr, I,
-                         H, Y);
-    }
-    LAUNCH_CHECK();
-  }
+  if ((r = routed_fwd<D>(p, s, T, x, st, true)) != MOE_OK) return r;
   if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
   {
-    StageTimer st(p, s, MOE_STAGE_COMBINE_FWD);
-    hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, Y, inv, topw,
-                       sY, c.shared_expert_scale, T, k, H, out);
+    StageTimer tm(p, s, MOE_STAGE_COMBINE_FWD);
+    hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, st.Y, st.inv,
+                       st.w, sY, c.shared_expert_scale, T, k, H, out);
     LAUNCH_CHECK();
   }
   {
-    StageTimer st(p, s, MOE_STAGE_LOSSES);
-    hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, s,
-                       (const float*)(saved + L.f[MOE_SAVED_MEAN_PROB]), counts,
-                       (const float*)(saved + L.f[MOE_SAVED_LSE]), T, E, k, c.aux_switch_coef,
-                       c.aux_sqprob_coef, aux, z);
+    StageTimer tm(p, s, MOE_STAGE_LOSSES);
+    hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, s, st.P, st.counts, st.lse, T, E, k,
+                       c.aux_switch_coef, c.aux_sqprob_coef, aux, z);
     LAUNCH_CHECK();
   }
   return MOE_OK;
@@ -551,22 +622,30 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
             I = c.intermediate, S = c.shared_intermediate;
   const int Epad = round8(E);
   const int64_t TK = T64 * k;
-  const SavedLayout L = p->saved_layout(T64);
   const WsLayout W = p->ws_layout(T64);
-  const int* counts = (const int*)(saved + L.f[MOE_SAVED_COUNTS]);
-  const int* offsets = (const int*)(saved + L.f[MOE_SAVED_OFFSETS]);
-  const int* tprefix = (const int*)(saved + L.tile_prefix) + tile_slot(CB::BM) * (E + 1);
-  const int* inv = (const int*)(saved + L.f[MOE_SAVED_INV_PERM]);
-  const int* idx = (const int*)(saved + L.f[MOE_SAVED_TOPK_IDX]);
-  const float* topw = (const float*)(saved + L.f[MOE_SAVED_TOPK_W]);
-  const float* probs = (const float*)(saved + L.f[MOE_SAVED_PROBS]);
-  const float* lse = (const float*)(saved + L.f[MOE_SAVED_LSE]);
-  const float* P = (const float*)(saved + L.f[MOE_SAVED_MEAN_PROB]);
-  const D* xp = (const D*)(saved + L.f[MOE_SAVED_X_PERM]);
-  const D* G = (const D*)(saved + L.f[MOE_SAVED_GATE_ACT]);
-  const D* U = (const D*)(saved + L.f[MOE_SAVED_UP_ACT]);
-  const D* A = (const D*)(saved + L.f[MOE_SAVED_SWIGLU]);
-  const D* Y = (const D*)(saved + L.f[MOE_SAVED_EXPERT_OUT]);
+  // With recompute_activations `saved` holds the routing state only: the
+  // expert activations are rebuilt in the workspace by the forward's own
+  // launches (same kernels, same inputs, so the same bits) before use.
+  const bool recompute = c.recompute_activations != 0;
+  const SavedLayout LR = p->kept_layout(T64);
+  const SavedLayout LA = recompute ? p->saved_layout(T64, moe_plan::Keep::All) : LR;
+  char* rb = const_cast<char*>(saved);
+  char* ab = recompute ? ws + W.recomp : rb;
+  const State<D> st(rb, LR, ab, LA);
+  const int* counts = st.counts;
+  const int* offsets = st.offsets;
+  const int* tprefix = st.tprefix + tile_slot(CB::BM) * (E + 1);
+  const int* inv = st.inv;
+  const int* idx = st.idx;
+  const float* topw = st.w;
+  const float* probs = st.probs;
+  const float* lse = st.lse;
+  const float* P = st.P;
+  const D* xp = st.xp;
+  const D* G = st.G;
+  const D* U = st.U;
+  const D* A = st.A;
+  const D* Y = st.Y;
   float* dw = (float*)(ws + W.dw);
   D* dY = (D*)(ws + W.dY);
   D* dG = (D*)(ws + W.dG);
@@ -593,11 +672,16 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
       HIP_TRY(hipEventRecord(p->fork, s));
       HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
     }
-    StageTimer st(p, ss, MOE_STAGE_SHARED_BWD);
+    if (recompute) {
+      StageTimer tm(p, ss, MOE_STAGE_RECOMPUTE);
+      shared_fwd<D>(p, ss, T, x, w, st.sG, st.sU, st.sA, nullptr);
+      LAUNCH_CHECK();
+    }
+    StageTimer tm(p, ss, MOE_STAGE_SHARED_BWD);
     float* partial_sh = (float*)(ws + W.splitk_shared);
-    const D* sG = (const D*)(saved + L.sG);
-    const D* sU = (const D*)(saved + L.sU);
-    const D* sA = (const D*)(saved + L.sA);
+    const D* sG = st.sG;
+    const D* sU = st.sU;
+    const D* sA = st.sA;
     D* sdG = (D*)(ws + W.sdG);
     D* sdU = (D*)(ws + W.sdU);
     dxs = (D*)(ws + W.dxs);
@@ -613,6 +697,10 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                              (D*)g->shared_up, partial_sh);
     LAUNCH_CHECK();
     if (ss != s) HIP_TRY(hipEventRecord(p->join, ss));
+  }
+  if (recompute) {
+    moe_status r = routed_fwd<D>(p, s, T, x, st, false);
+    if (r != MOE_OK) return r;
   }
   {
     StageTimer st(p, s, MOE_STAGE_COMBINE_BWD);
@@ -711,6 +799,9 @@ moe_status validate_config(const moe_config* c) {
                 c->experts_per_tok);
   if (!(c->router_temperature > 0.0f))
     return fail(MOE_ERR_INVALID, "router_temperature must be positive");
+  if (c->recompute_activations != 0 && c->recompute_activations != 1)
+    return fail(MOE_ERR_INVALID, "recompute_activations (%d) must be 0 or 1",
+                c->recompute_activations);
   return MOE_OK;
 }
 
@@ -792,7 +883,7 @@ moe_status moe_plan_destroy(moe_plan* p) {
 
 size_t moe_saved_bytes(const moe_plan* p, int64_t T) {
   if (!p || T < 0) return 0;
-  return p->saved_layout(T).total;
+  return p->kept_layout(T).total;
 }
 
 size_t moe_workspace_bytes(const moe_plan* p, int64_t T) {
@@ -805,7 +896,7 @@ moe_status moe_saved_field_range(const moe_plan* p, int64_t T, int32_t field, si
   if (!p) return fail(MOE_ERR_INVALID, "plan is NULL");
   if (field < 0 || field >= MOE_SAVED_NUM_FIELDS)
     return fail(MOE_ERR_INVALID, "unknown saved field %d", field);
-  const SavedLayout L = p->saved_layout(T);
+  const SavedLayout L = p->kept_layout(T);
   if (offset) *offset = L.f[field];
   if (bytes) *bytes = L.fbytes[field];
   return MOE_OK;
@@ -888,7 +979,7 @@ moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const flo
   if (!logits || !saved || !workspace) return fail(MOE_ERR_INVALID, "a required pointer is NULL");
   hipStream_t s = (hipStream_t)stream;
   HIP_TRY(hipSetDevice(p->device));
-  const SavedLayout L = p->saved_layout(T);
+  const SavedLayout L = p->kept_layout(T);
   const WsLayout W = p->ws_layout(T);
   char* sv = (char*)saved;
   HIP_TRY(hipMemcpyAsync(sv + L.f[MOE_SAVED_LOGITS], logits,
@@ -902,7 +993,7 @@ const char* moe_stage_name(int32_t stage) {
   static const char* names[MOE_NUM_STAGES] = {
       "router_gemm", "route", "dispatch", "gather", "gateup_fwd", "down_fwd", "shared_fwd",
       "combine_fwd", "losses", "combine_bwd", "down_dgrad", "down_wgrad", "gateup_dgrad",
-      "gateup_wgrad", "shared_bwd", "router_bwd", "dx"};
+      "gateup_wgrad", "shared_bwd", "router_bwd", "dx", "recompute"};
   if (stage < 0 || stage >= MOE_NUM_STAGES) return "unknown";
   return names[stage];
 }

@@ -48,6 +48,10 @@ class MoeConfig:
     aux_sqprob_coef: float = 1.0
     shared_expert_scale: float = 1.0
     router_bias: bool = False
+    # trainer.activation_checkpointing covering this layer
+    # (src/config/activation_checkpointing.rs:25-35): keep only the routing
+    # state between forward and backward and recompute the expert activations.
+    recompute_activations: bool = False
 
     def has_shared_expert(self) -> bool:
         return True if self.shared_expert_enabled is None else bool(self.shared_expert_enabled)
@@ -103,6 +107,7 @@ class Plan:
         c.shared_expert_scale = cfg.shared_expert_scale
         c.aux_switch_coef = cfg.aux_switch_coef
         c.aux_sqprob_coef = cfg.aux_sqprob_coef
+        c.recompute_activations = int(cfg.recompute_activations)
         self.c = c
         h = ctypes.c_void_p()
         idx = self.device.index if self.device.index is not None else torch.cuda.current_device()

@@ -17,7 +17,8 @@ def rel(a, b):
 
 class Case:
     def __init__(self, T, H, E, k, I, S=0, dtype="f32", w_std=0.1, seed=0, bias=None,
-                 norm_topk=False, tau=1.0, shared_scale=1.0, aux_switch=1.0, aux_sqprob=1.0):
+                 norm_topk=False, tau=1.0, shared_scale=1.0, aux_switch=1.0, aux_sqprob=1.0,
+                 recompute=False):
         self.T, self.H, self.E, self.k, self.I, self.S = T, H, E, k, I, S
         self.dtype = dtype
         self.tdtype = torch.float32 if dtype == "f32" else torch.bfloat16
@@ -27,7 +28,8 @@ class Case:
                              shared_expert_enabled=S > 0, shared_intermediate_size=S or None,
                              router_temperature=tau, norm_topk_prob=norm_topk,
                              aux_switch_coef=aux_switch, aux_sqprob_coef=aux_sqprob,
-                             shared_expert_scale=shared_scale, router_bias=bias is not None)
+                             shared_expert_scale=shared_scale, router_bias=bias is not None,
+                             recompute_activations=recompute)
         self.ocfg = mo.make_cfg(T, H, E, k, I, S, norm_topk=norm_topk, has_bias=bias is not None,
                                 tau=tau, shared_scale=shared_scale, aux_switch=aux_switch,
                                 aux_sqprob=aux_sqprob)

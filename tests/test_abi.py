@@ -5,6 +5,7 @@ and the host-side config validation follows the reference's messages
 import ctypes
 import os
 import re
+import subprocess
 
 import pytest
 
@@ -30,11 +31,31 @@ def test_library_exports_every_declared_symbol():
     assert sorted(_lib.EXPORTED) == names
 
 
-def test_struct_layouts_match_header():
-    # moe_config: 8 int32 + 4 float; moe_weights / moe_grads: 8 pointers
-    assert ctypes.sizeof(_lib.MoeConfigC) == 48
-    assert ctypes.sizeof(_lib.MoeWeightsC) == 64
-    assert ctypes.sizeof(_lib.MoeGradsC) == 64
+def test_struct_layouts_match_header(tmp_path):
+    # every field offset and struct size of the ctypes mirror equals what a C
+    # compiler makes of include/moe_hip.h
+    structs = {"moe_config": _lib.MoeConfigC, "moe_weights": _lib.MoeWeightsC,
+               "moe_grads": _lib.MoeGradsC}
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "moe_hip.h"', "int main(void) {"]
+    for cname, py in structs.items():
+        lines.append(f'  printf("{cname} size %zu\\n", sizeof({cname}));')
+        for f, _ in py._fields_:
+            lines.append(f'  printf("{cname} {f} %zu\\n", offsetof({cname}, {f}));')
+    lines += ["  return 0;", "}"]
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)],
+                   check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                               text=True).stdout.splitlines():
+        cname, f, v = line.split()
+        got[(cname, f)] = int(v)
+    for cname, py in structs.items():
+        assert got[(cname, "size")] == ctypes.sizeof(py), cname
+        for f, _ in py._fields_:
+            assert got[(cname, f)] == getattr(py, f).offset, (cname, f)
 
 
 def test_config_defaults_and_names():
@@ -47,8 +68,9 @@ def test_config_defaults_and_names():
     assert c.router_temperature == 1.0 and c.shared_expert_scale == 1.0
     assert c.aux_switch_coef == 1.0 and c.aux_sqprob_coef == 1.0
     assert c.norm_topk_prob == 0 and c.has_router_bias == 0
+    assert c.recompute_activations == 0
     names = [L.moe_stage_name(i).decode() for i in range(_lib.NUM_STAGES)]
-    assert names[0] == "router_gemm" and names[-1] == "dx"
+    assert names[0] == "router_gemm" and names[-2:] == ["dx", "recompute"]
     assert L.moe_stage_name(_lib.NUM_STAGES).decode() == "unknown"
     assert b"gfx950" in L.moe_version()
 

@@ -253,3 +253,34 @@ def test_layer_under_no_grad_matches_grad_path():
     assert out_g.requires_grad and not out_n.requires_grad
     assert torch.equal(out_g.detach(), out_n)
     assert torch.equal(aux_g.detach(), aux_n) and torch.equal(z_g.detach(), z_n)
+
+
+# ---------------------------------------------------------------- recompute policy
+
+@pytest.mark.parametrize("dtype,T", [("f32", 300), ("bf16", 300), ("bf16", 40), ("bf16", 9)])
+def test_recompute_activations_is_bitwise_equal(dtype, T):
+    # recompute_activations keeps only the routing state; the backward rebuilds
+    # the activations with the forward's own launches, so every output and
+    # gradient is the same bits as with the activations kept
+    kw = dict(T=T, H=128, E=16, k=2, I=64, S=64, dtype=dtype, w_std=0.05, seed=13)
+    keep = Case(**kw)
+    rec = Case(recompute=True, **kw)
+    a = gpu_run(keep, d_aux=0.01, d_z=0.001)
+    b = gpu_run(rec, d_aux=0.01, d_z=0.001)
+    for n in ("out", "aux", "z", "dx", "router", "gate", "up", "down", "shared_gate",
+              "shared_up", "shared_down", "has_grad", "topk_idx", "perm"):
+        np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+
+
+def test_recompute_shrinks_saved_state():
+    dev = torch.device("cuda:0")
+    kw = dict(hidden_size=256, num_experts=16, experts_per_tok=2, intermediate_size=128,
+              shared_intermediate_size=128)
+    keep = Plan(MoeConfig(**kw), torch.bfloat16, dev)
+    rec = Plan(MoeConfig(recompute_activations=True, **kw), torch.bfloat16, dev)
+    T = 1000
+    # routing state only: no [T*k, H] / [T*k, I] / [T, S] activation is kept
+    act = 2 * (T * 2 * 256 * 2 + T * 2 * 128 * 3 + T * 128 * 3)
+    assert keep.saved_bytes(T) - rec.saved_bytes(T) >= act
+    assert rec.saved_bytes(T) < 40 * T * 16
+    assert rec.workspace_bytes(T) > keep.workspace_bytes(T)
