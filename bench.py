@@ -201,6 +201,10 @@ def main():
                          "torch.matmul = hipBLASLt, and a 1 GiB device copy) and exit")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--block", action="store_true",
+                    help="time the block's whole MoE sub-block (post_attention_layernorm "
+                         "RMSNorm + MoE layer + residual add) through moe_block_forward / "
+                         "moe_block_backward")
     ap.add_argument("--recompute", action="store_true",
                     help="keep only the routing state between forward and backward and "
                          "recompute the expert activations in the backward (the plan's "
@@ -251,8 +255,9 @@ def main():
     cfg = MoeConfig(hidden_size=H, num_experts=E, experts_per_tok=k, intermediate_size=I,
                     shared_expert_enabled=S > 0, shared_intermediate_size=S or None,
                     load_balance_alpha=wl.alpha, router_bias=bias is not None,
-                    recompute_activations=bool(args.recompute))
+                    recompute_activations=bool(args.recompute), fused_block=bool(args.block))
     plan = Plan(cfg, dtype, dev)
+    norm_w = (1.0 + 0.1 * torch.randn(H, generator=gen, device=dev)).to(dtype) if args.block else None
     w, _keep_w = plan.weights_struct(router, list(gate.unbind(0)), list(up.unbind(0)),
                                      list(down.unbind(0)), bias, shared)
     out = torch.empty_like(x)
@@ -270,15 +275,30 @@ def main():
         d_z = torch.tensor(0.0, device=dev)                  # z-loss weight 0 in the timed runs
         has_grad = torch.empty(E, dtype=torch.uint8, device=dev)
 
+    if args.block:
+        d_norm_w = torch.empty_like(norm_w)
+
+    def fwd(need_grad=True):
+        if args.block:  # x is the block input h; out = MoE(RMSNorm(h)) + h
+            plan.block_forward(x, norm_w, w, out=out, saved=saved if need_grad else None, aux=aux,
+                               z=z, need_grad=need_grad)
+        else:
+            plan.forward(x, w, out=out, saved=saved if need_grad else None, aux=aux, z=z,
+                         need_grad=need_grad)
+
     def step():
         if wl.backward:
-            plan.forward(x, w, out=out, saved=saved, aux=aux, z=z)
-            plan.backward(x, dout, w, g, saved, dx=dx, d_aux=d_aux, d_z=d_z, has_grad=has_grad)
+            fwd()
+            if args.block:
+                plan.block_backward(x, norm_w, dout, w, g, saved, dh=dx, d_norm_w=d_norm_w,
+                                    d_aux=d_aux, d_z=d_z, has_grad=has_grad)
+            else:
+                plan.backward(x, dout, w, g, saved, dx=dx, d_aux=d_aux, d_z=d_z, has_grad=has_grad)
         else:  # forward-only call: no saved state, no gate / up pre-activations
-            plan.forward(x, w, out=out, aux=aux, z=z, need_grad=False)
+            fwd(need_grad=False)
 
     dominant = "gateup_fwd"
-    plan.forward(x, w, out=out, saved=saved, aux=aux, z=z)  # realized routing (untimed)
+    fwd()  # realized routing (untimed)
     counts = plan.saved_field(saved, T, "counts").cpu()
     for _ in range(args.warmup):
         step()
@@ -359,6 +379,8 @@ def main():
                    "parallelism": "single GPU", "routing": wl.skew, **skew_info,
                    "max_expert_tokens": int(counts.max()), "empty_experts": int((counts == 0).sum()),
                    "activations": "recomputed in backward" if args.recompute else "kept",
+                   "scope": ("block MoE sub-block: RMSNorm + layer + residual" if args.block
+                             else "MoE layer"),
                    "saved_MB_per_layer": round(plan.saved_bytes(T) / 1e6, 1),
                    "workspace_MB": round(plan.workspace_bytes(T) / 1e6, 1)},
         "roofline": roof,

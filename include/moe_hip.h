@@ -69,6 +69,12 @@ typedef struct {
                                    first (trainer.activation_checkpointing covering
                                    this layer, src/config/activation_checkpointing.rs
                                    :25-35, src/model/recompute/segment.rs:58-170)  */
+  int32_t fused_block;          /* 1: the plan runs the block's whole MoE sub-block
+                                   through moe_block_forward / moe_block_backward:
+                                   post_attention_layernorm (RMSNorm) before the
+                                   layer and the residual add after it
+                                   (src/model.rs:2792-2800, :2822-2826)           */
+  float rms_norm_eps;           /* RMSNorm eps (cfg.rms_norm_eps); fused_block only */
 } moe_config;
 
 /* Fills cfg with the documented defaults: tau = 1, s = 1, c_sw = c_sq = 1,
@@ -136,6 +142,27 @@ moe_status moe_backward(moe_plan* plan, void* stream, int64_t num_tokens, const 
                         const moe_weights* w, const void* saved, void* workspace, void* dx,
                         const moe_grads* g, uint8_t* has_grad);
 
+/* The MoE sub-block of a decoder block, for plans created with fused_block = 1
+ * (src/model.rs:2792-2800 MLA arm, :2822-2826 legacy arm: residual = h;
+ * x = post_attention_layernorm(h); (y, aux, z) = ffn(x); out = y + residual).
+ * h [T, H]; norm_weight [H] (dtype) is post_attention_layernorm.weight;
+ * RMSNorm(h) = h / sqrt(mean(h^2) + rms_norm_eps) * norm_weight with fp32
+ * statistics.  The residual add is fused into the combine: out is rounded once.
+ * `saved` as for moe_forward (NULL: forward only). */
+moe_status moe_block_forward(moe_plan* plan, void* stream, int64_t num_tokens, const void* h,
+                             const void* norm_weight, const moe_weights* w, void* out,
+                             float* aux_loss, float* z_loss, void* saved, void* workspace);
+
+/* Backward of moe_block_forward: dh [T, H] = d_out (the residual's path) +
+ * the RMSNorm backward of the layer's input gradient; d_norm_weight [H]
+ * (dtype, overwritten) = sum_t dx_t * h_t * rstd_t, reduced in a fixed order.
+ * The layer's weight gradients and has_grad as for moe_backward. */
+moe_status moe_block_backward(moe_plan* plan, void* stream, int64_t num_tokens,
+                              const void* d_out, const float* d_aux, const float* d_z,
+                              const void* h, const void* norm_weight, const moe_weights* w,
+                              const void* saved, void* workspace, void* dh,
+                              void* d_norm_weight, const moe_grads* g, uint8_t* has_grad);
+
 /* Routing and dispatch only, from given fp32 logits [T, E] (no reference
  * counterpart; lets a caller check top-k and the permutation bit-exactly on
  * identical logits).  Fills the routing fields of `saved`. */
@@ -160,6 +187,8 @@ typedef enum {
   MOE_SAVED_UP_ACT,       /* dtype [T*k, I]: x W_u^T */
   MOE_SAVED_SWIGLU,       /* dtype [T*k, I]: silu(gate) * up */
   MOE_SAVED_EXPERT_OUT,   /* dtype [T*k, H]: per-assignment expert output */
+  MOE_SAVED_RSTD,         /* fp32 [T]: 1 / RMS of h (fused_block plans only) */
+  MOE_SAVED_NORM_X,       /* dtype [T, H]: RMSNorm(h), the layer input (fused_block only) */
   MOE_SAVED_NUM_FIELDS
 } moe_saved_field;
 moe_status moe_saved_field_range(const moe_plan* plan, int64_t num_tokens, int32_t field,
@@ -173,7 +202,7 @@ typedef enum {
   MOE_STAGE_GATEUP_FWD, MOE_STAGE_DOWN_FWD, MOE_STAGE_SHARED_FWD, MOE_STAGE_COMBINE_FWD,
   MOE_STAGE_LOSSES, MOE_STAGE_COMBINE_BWD, MOE_STAGE_DOWN_DGRAD, MOE_STAGE_DOWN_WGRAD,
   MOE_STAGE_GATEUP_DGRAD, MOE_STAGE_GATEUP_WGRAD, MOE_STAGE_SHARED_BWD, MOE_STAGE_ROUTER_BWD,
-  MOE_STAGE_DX, MOE_STAGE_RECOMPUTE, MOE_NUM_STAGES
+  MOE_STAGE_DX, MOE_STAGE_RECOMPUTE, MOE_STAGE_NORM_FWD, MOE_STAGE_NORM_BWD, MOE_NUM_STAGES
 } moe_stage;
 const char* moe_stage_name(int32_t stage);
 moe_status moe_plan_set_profiling(moe_plan* plan, int32_t stage_mask);

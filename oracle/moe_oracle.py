@@ -177,3 +177,51 @@ class MoeOracle:
                               _ptr(g["shared_up"]), _ptr(g["shared_down"]), _ptr(has_grad))
         g["has_grad"] = has_grad
         return g
+
+
+# ---------------------------------------------------------------- block path
+# The MoE sub-block of a decoder block (reference src/model.rs:2792-2800 MLA
+# arm, :2822-2826 legacy arm): residual = h; x = post_attention_layernorm(h);
+# (y, aux, z) = MoE(x); out = y + residual.  post_attention_layernorm is
+# boostr::nn::RmsNorm (src/model.rs:500-512: weight [H], eps = cfg.rms_norm_eps);
+# its formula is restated as x = h * rstd * w, rstd = 1 / sqrt(mean(h^2) + eps).
+
+def rmsnorm_forward(h, w, eps):
+    """(x, rstd) in float64, per row of h [T, H]."""
+    h = np.asarray(h, np.float64)
+    w = np.asarray(w, np.float64)
+    rstd = 1.0 / np.sqrt((h * h).mean(axis=-1) + eps)
+    return h * rstd[:, None] * w, rstd
+
+
+def rmsnorm_backward(dx, h, w, rstd):
+    """(dh, dw) of x = h * rstd * w for the upstream gradient dx."""
+    h = np.asarray(h, np.float64)
+    w = np.asarray(w, np.float64)
+    xh = h * rstd[:, None]
+    gw = np.asarray(dx, np.float64) * w
+    mean = (xh * gw).mean(axis=-1, keepdims=True)
+    return rstd[:, None] * (gw - xh * mean), (np.asarray(dx, np.float64) * xh).sum(axis=0)
+
+
+class MoeBlockOracle:
+    """post_attention_layernorm -> MoE layer (MoeOracle) -> residual add."""
+
+    def __init__(self, cfg, eps, precision=64):
+        self.moe = MoeOracle(cfg, precision)
+        self.eps = eps
+
+    def forward(self, h, norm_weight, wr, wg, wu, wd, bias=None, swg=None, swu=None, swd=None,
+                logits_in=None):
+        self.hin = np.asarray(h, np.float64).reshape(-1, self.moe.cfg.H)
+        self.nw = np.asarray(norm_weight, np.float64)
+        x, self.rstd = rmsnorm_forward(self.hin, self.nw, self.eps)
+        y, aux, z = self.moe.forward(x, wr, wg, wu, wd, bias, swg, swu, swd, logits_in=logits_in)
+        return y + self.hin, aux, z
+
+    def backward(self, dout, d_aux=0.0, d_z=0.0, fill=np.nan):
+        g = self.moe.backward(dout, d_aux, d_z, fill)
+        dh, dw = rmsnorm_backward(g["x"], self.hin, self.nw, self.rstd)
+        g["h"] = np.asarray(dout, np.float64).reshape(dh.shape) + dh
+        g["norm_weight"] = dw
+        return g

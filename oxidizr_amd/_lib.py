@@ -13,16 +13,17 @@ MOE_DTYPE_F32 = 0
 MOE_DTYPE_BF16 = 1
 
 SAVED_FIELDS = ["logits", "probs", "lse", "topk_idx", "topk_w", "counts", "offsets", "perm",
-                "inv_perm", "mean_prob", "x_perm", "gate_act", "up_act", "swiglu", "expert_out"]
+                "inv_perm", "mean_prob", "x_perm", "gate_act", "up_act", "swiglu", "expert_out",
+                "rstd", "norm_x"]
 
 EXPORTED = [
     "moe_config_default", "moe_plan_create", "moe_plan_destroy", "moe_saved_bytes",
     "moe_workspace_bytes", "moe_forward", "moe_backward", "moe_route_from_logits",
     "moe_saved_field_range", "moe_stage_name", "moe_plan_set_profiling", "moe_plan_stage_times",
-    "moe_plan_set_shared_overlap",
+    "moe_plan_set_shared_overlap", "moe_block_forward", "moe_block_backward",
     "moe_last_error", "moe_version",
 ]
-NUM_STAGES = 18
+NUM_STAGES = 20
 
 
 class MoeConfigC(ctypes.Structure):
@@ -33,7 +34,8 @@ class MoeConfigC(ctypes.Structure):
         ("norm_topk_prob", ctypes.c_int32), ("has_router_bias", ctypes.c_int32),
         ("router_temperature", ctypes.c_float), ("shared_expert_scale", ctypes.c_float),
         ("aux_switch_coef", ctypes.c_float), ("aux_sqprob_coef", ctypes.c_float),
-        ("recompute_activations", ctypes.c_int32),
+        ("recompute_activations", ctypes.c_int32), ("fused_block", ctypes.c_int32),
+        ("rms_norm_eps", ctypes.c_float),
     ]
 
 
@@ -85,6 +87,12 @@ def load():
     L.moe_backward.argtypes = [_vp, _vp, i64, _vp, _vp, _vp, _vp, P(MoeWeightsC), _vp, _vp, _vp,
                                P(MoeGradsC), _vp]
     L.moe_backward.restype = i32
+    L.moe_block_forward.argtypes = [_vp, _vp, i64, _vp, _vp, P(MoeWeightsC), _vp, _vp, _vp, _vp,
+                                    _vp]
+    L.moe_block_forward.restype = i32
+    L.moe_block_backward.argtypes = [_vp, _vp, i64, _vp, _vp, _vp, _vp, _vp, P(MoeWeightsC), _vp,
+                                     _vp, _vp, _vp, P(MoeGradsC), _vp]
+    L.moe_block_backward.restype = i32
     L.moe_route_from_logits.argtypes = [_vp, _vp, i64, _vp, _vp, _vp]
     L.moe_route_from_logits.restype = i32
     L.moe_saved_field_range.argtypes = [_vp, i64, i32, P(sz), P(sz)]

@@ -537,13 +537,15 @@ __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGr
 }
 
 // ------------------------------------------------------------------ combine
-// out[t] = sum_j w[t, j] * Y[inv_perm[t, j]] (+ s * Ys[t]); one wave per token.
+// out[t] = sum_j w[t, j] * Y[inv_perm[t, j]] (+ s * Ys[t]) (+ resid[t]), added in
+// that order in fp32 and rounded once; one wave per token.
 template <typename T>
 __global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
                                                      const int* __restrict__ inv_perm,
                                                      const float* __restrict__ w,
                                                      const T* __restrict__ Ys, float s, int Tn,
-                                                     int k, int H, T* __restrict__ out) {
+                                                     int k, int H, const T* __restrict__ resid,
+                                                     T* __restrict__ out) {
   constexpr int V = Vec16<T>::N;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
@@ -569,6 +571,11 @@ __global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
       unpack16(ld16(Ys + (int64_t)t * H + c * V), y, T());
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[i] += s * y[i];
+    }
+    if (resid) {  // the block's residual add, fused
+      unpack16(ld16(resid + (int64_t)t * H + c * V), y, T());
+#pragma unroll
+      for (int i = 0; i < V; ++i) acc[i] += y[i];
     }
     st16(out + (int64_t)t * H + c * V, pack16(acc, T()));
   }
@@ -897,6 +904,151 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
 __global__ void k_has_grad(const int* __restrict__ counts, int E, uint8_t* __restrict__ has_grad) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e < E) has_grad[e] = counts[e] > 0 ? 1 : 0;
+}
+
+// ------------------------------------------------------------------ fused RMSNorm (block path)
+// The MoE sub-block of a decoder block (src/model.rs:2792-2800):
+//   x = RMSNorm(h) = h * rstd * w,  rstd = 1 / sqrt(mean_i h_i^2 + eps),
+//   out = MoE(x) + h  (the residual add is fused into k_combine_fwd).
+// Statistics and products in fp32, one rounding of x to the dtype; one wave
+// per token row, lanes over 16-byte vectors.
+template <typename T>
+__global__ __launch_bounds__(256) void k_rmsnorm_fwd(const T* __restrict__ h,
+                                                     const T* __restrict__ w, float eps, int Tn,
+                                                     int H, T* __restrict__ x,
+                                                     float* __restrict__ rstd) {
+  constexpr int V = Vec16<T>::N;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  const int lane = threadIdx.x & 63;
+  const T* row = h + (int64_t)t * H;
+  float ss = 0.0f;
+  for (int c = lane; c < H / V; c += 64) {
+    float v[V];
+    unpack16(ld16(row + c * V), v, T());
+#pragma unroll
+    for (int i = 0; i < V; ++i) ss += v[i] * v[i];
+  }
+  ss = wave_sum(ss);
+  const float r = 1.0f / sqrtf(ss / (float)H + eps);
+  if (lane == 0) rstd[t] = r;
+  for (int c = lane; c < H / V; c += 64) {
+    float v[V], g[V];
+    unpack16(ld16(row + c * V), v, T());
+    unpack16(ld16(w + c * V), g, T());
+#pragma unroll
+    for (int i = 0; i < V; ++i) v[i] = v[i] * r * g[i];
+    st16(x + (int64_t)t * H + c * V, pack16(v, T()));
+  }
+}
+
+// RMSNorm backward with the residual's gradient:
+//   dh = d_out + rstd * (w * dx - xhat * mean_i(xhat_i * w_i * dx_i)),  xhat = h * rstd,
+// and per-block partial rows of the weight gradient,
+//   part[b][i] = sum over the block's rows (ascending) of dx_i * xhat_i.
+// One block of 256 threads per kRmsRows consecutive rows; thread j owns the
+// 8-column chunks j, j + 256, ... (NCH of them, H <= 2048 * NCH).
+constexpr int kRmsRows = 8;
+template <typename T, int NCH>
+__global__ __launch_bounds__(256) void k_rmsnorm_bwd(const T* __restrict__ dx,
+                                                     const T* __restrict__ h,
+                                                     const T* __restrict__ w,
+                                                     const float* __restrict__ rstd,
+                                                     const T* __restrict__ dout, int Tn, int H,
+                                                     T* __restrict__ dh, float* __restrict__ part) {
+  __shared__ float red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = H / 8;
+  float wv[NCH][8], acc[NCH][8];
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int ch = tid + c * 256;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) wv[c][i] = acc[c][i] = 0.0f;
+    if (ch < nch) load8(w + ch * 8, wv[c]);
+  }
+  const int t0 = blockIdx.x * kRmsRows, t1 = min(Tn, t0 + kRmsRows);
+  // dx and h of the next row are requested before this row's reduction
+  float dn[NCH][8], hn[NCH][8];
+  auto load_row = [&](int t) {
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = tid + c * 256;
+      if (ch < nch) {
+        load8(dx + (int64_t)t * H + ch * 8, dn[c]);
+        load8(h + (int64_t)t * H + ch * 8, hn[c]);
+      }
+    }
+  };
+  if (t0 < t1) load_row(t0);
+  for (int t = t0; t < t1; ++t) {
+    const float r = rstd[t];
+    float d[NCH][8], xh[NCH][8];
+#pragma unroll
+    for (int c = 0; c < NCH; ++c)
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        d[c][i] = dn[c][i];
+        xh[c][i] = hn[c][i];
+      }
+    if (t + 1 < t1) load_row(t + 1);
+    float dot = 0.0f;
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = tid + c * 256;
+      if (ch < nch) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          xh[c][i] *= r;
+          dot += xh[c][i] * wv[c][i] * d[c][i];
+        }
+      }
+    }
+    dot = wave_sum(dot);
+    if (lane == 0) red[wave] = dot;
+    __syncthreads();
+    const float mean = ((red[0] + red[1]) + (red[2] + red[3])) / (float)H;
+    __syncthreads();  // red is rewritten by the next row
+#pragma unroll
+    for (int c = 0; c < NCH; ++c) {
+      const int ch = tid + c * 256;
+      if (ch < nch) {
+        float g[8], o[8];
+        load8(dout + (int64_t)t * H + ch * 8, g);
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          o[i] = g[i] + r * (wv[c][i] * d[c][i] - xh[c][i] * mean);
+          acc[c][i] += d[c][i] * xh[c][i];
+        }
+        store8(dh + (int64_t)t * H + ch * 8, o);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int ch = tid + c * 256;
+    if (ch < nch) store8(part + (int64_t)blockIdx.x * H + ch * 8, acc[c]);
+  }
+}
+
+// out[g][i] = sum of in[r][i] over the rows r of group g (rpg rows, ascending);
+// 8 columns per thread.  Applied level by level, it reduces partial rows in a
+// fixed tree, independent of scheduling.
+template <typename OUT>
+__global__ __launch_bounds__(256) void k_rowsum(const float* __restrict__ in, int R, int H,
+                                                int rpg, OUT* __restrict__ out) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 8;
+  if (i >= H) return;
+  const int g = blockIdx.y, r0 = g * rpg, r1 = min(R, r0 + rpg);
+  float acc[8], v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+  for (int r = r0; r < r1; ++r) {
+    load8(in + (int64_t)r * H + i, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] += v[e];
+  }
+  store8(out + (int64_t)g * H + i, acc);
 }
 
 // ------------------------------------------------------------------ small-token forward

@@ -68,7 +68,7 @@ struct WsLayout {
   size_t block_hist, block_base, colpart, sY, infer;
   // backward
   size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
-      recomp;
+      recomp, dxm, dwn, dwn_a, dwn_b;
   size_t total;
 };
 
@@ -186,6 +186,9 @@ struct moe_plan {
     fld(MOE_SAVED_UP_ACT, pre ? b * TK * I : 0);
     fld(MOE_SAVED_SWIGLU, act ? b * TK * I : 0);
     fld(MOE_SAVED_EXPERT_OUT, act ? b * TK * H : 0);
+    const bool blk = cfg.fused_block != 0 && act;
+    fld(MOE_SAVED_RSTD, blk ? 4 * (size_t)T : 0);
+    fld(MOE_SAVED_NORM_X, blk ? b * T * H : 0);
     L.sGbytes = L.sUbytes = pre ? b * T * S : 0;
     L.sAbytes = act ? b * T * S : 0;
     L.sG = c.take(L.sGbytes);
@@ -234,6 +237,14 @@ struct moe_plan {
                                  : splitk_bytes<bf16_t>(cfg, T, true));
     // a recomputing backward rebuilds every activation here first
     L.recomp = g.take(cfg.recompute_activations ? saved_layout(T, Keep::All).total : 0);
+    // fused block: the layer's input gradient, then the RMSNorm weight
+    // gradient's partial rows and two levels of their fixed-order reduction
+    const bool blk = cfg.fused_block != 0;
+    const int nrow = ceil_div(T, kRmsRows);
+    L.dxm = g.take(blk ? b * T * H : 0);
+    L.dwn = g.take(blk ? 4 * (size_t)nrow * H : 0);
+    L.dwn_a = g.take(blk ? 4 * (size_t)ceil_div(nrow, 16) * H : 0);
+    L.dwn_b = g.take(blk ? 4 * (size_t)ceil_div(nrow, 256) * H : 0);
     L.total = f.off > g.off ? f.off : g.off;
     return L;
   }
@@ -532,7 +543,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
 template <typename D>
 moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                         const moe_weights* w, D* out, float* aux, float* z, char* saved,
-                        char* ws) {
+                        char* ws, const D* resid) {
   using CR = typename Tilings<D>::Router;
   using CG = typename Tilings<D>::GateUp;
   using CB = typename Tilings<D>::Big;
@@ -587,7 +598,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   {
     StageTimer tm(p, s, MOE_STAGE_COMBINE_FWD);
     hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, st.Y, st.inv,
-                       st.w, sY, c.shared_expert_scale, T, k, H, out);
+                       st.w, sY, c.shared_expert_scale, T, k, H, resid, out);
     LAUNCH_CHECK();
   }
   {
@@ -802,6 +813,12 @@ moe_status validate_config(const moe_config* c) {
   if (c->recompute_activations != 0 && c->recompute_activations != 1)
     return fail(MOE_ERR_INVALID, "recompute_activations (%d) must be 0 or 1",
                 c->recompute_activations);
+  if (c->fused_block != 0 && c->fused_block != 1)
+    return fail(MOE_ERR_INVALID, "fused_block (%d) must be 0 or 1", c->fused_block);
+  if (c->fused_block && !(c->rms_norm_eps >= 0.0f))
+    return fail(MOE_ERR_INVALID, "rms_norm_eps must be non-negative");
+  if (c->fused_block && c->hidden > 8192)
+    return fail(MOE_ERR_UNSUPPORTED, "fused_block supports hidden <= 8192 (got %d)", c->hidden);
   return MOE_OK;
 }
 
@@ -902,20 +919,74 @@ moe_status moe_saved_field_range(const moe_plan* p, int64_t T, int32_t field, si
   return MOE_OK;
 }
 
-moe_status moe_forward(moe_plan* p, void* stream, int64_t T, const void* x, const moe_weights* w,
-                       void* out, float* aux_loss, float* z_loss, void* saved, void* workspace) {
+}  // extern "C"
+
+namespace {
+
+// RMSNorm forward of the block path into (xn, rstd).
+template <typename D>
+void launch_norm_fwd(moe_plan* p, hipStream_t s, int T, const void* h, const void* nw, char* xn,
+                     float* rstd) {
+  StageTimer tm(p, s, MOE_STAGE_NORM_FWD);
+  hipLaunchKernelGGL(k_rmsnorm_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, (const D*)h,
+                     (const D*)nw, p->cfg.rms_norm_eps, T, p->cfg.hidden, (D*)xn, rstd);
+}
+
+// RMSNorm backward of the block path: dh and the weight gradient (partial
+// rows per kRmsRows tokens, then a fixed 16-ary reduction tree).
+template <typename D>
+void launch_norm_bwd(moe_plan* p, hipStream_t s, int T, const D* dxm, const void* h,
+                     const void* nw, const float* rstd, const void* dout, void* dh, void* dnw,
+                     char* ws, const WsLayout& W) {
+  StageTimer tm(p, s, MOE_STAGE_NORM_BWD);
+  const int H = p->cfg.hidden;
+  const int nrow = ceil_div(T, kRmsRows);
+  float* part = (float*)(ws + W.dwn);
+  auto bwd = [&](auto nch) {
+    constexpr int NCH = decltype(nch)::value;
+    hipLaunchKernelGGL((k_rmsnorm_bwd<D, NCH>), dim3(nrow), dim3(256), 0, s, dxm, (const D*)h,
+                       (const D*)nw, rstd, (const D*)dout, T, H, (D*)dh, part);
+  };
+  if (H <= 2048) bwd(std::integral_constant<int, 1>());
+  else if (H <= 4096) bwd(std::integral_constant<int, 2>());
+  else bwd(std::integral_constant<int, 4>());
+  const float* in = part;
+  float* bufs[2] = {(float*)(ws + W.dwn_a), (float*)(ws + W.dwn_b)};
+  int R = nrow, which = 0;
+  while (R > 16) {
+    const int G = ceil_div(R, 16);
+    hipLaunchKernelGGL(k_rowsum<float>, dim3(ceil_div(H, 2048), G), dim3(256), 0, s, in, R, H,
+                       16, bufs[which]);
+    in = bufs[which];
+    which ^= 1;
+    R = G;
+  }
+  hipLaunchKernelGGL(k_rowsum<D>, dim3(ceil_div(H, 2048), 1), dim3(256), 0, s, in, R, H, R,
+                     (D*)dnw);
+}
+
+// Shared argument checks and table upload of the forward entry points.
+// block: moe_block_forward (x is h, nw the RMSNorm weight).
+moe_status forward_entry(moe_plan* p, void* stream, int64_t T, const void* x, const void* nw,
+                         const moe_weights* w, void* out, float* aux_loss, float* z_loss,
+                         void* saved, void* workspace, bool block) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
   if ((st = check_tokens(T)) != MOE_OK) return st;
   if (!w) return fail(MOE_ERR_INVALID, "weights struct is NULL");
   const moe_config& c = p->cfg;
-  if (T > 0 && (!x || !out || !workspace || !w->router || !w->gate || !w->up || !w->down))
+  if (block && !c.fused_block)
+    return fail(MOE_ERR_INVALID, "moe_block_forward needs a plan created with fused_block = 1");
+  if (!block && c.fused_block)
+    return fail(MOE_ERR_INVALID, "the plan was created with fused_block = 1: call moe_block_forward");
+  if (T > 0 && (!x || !out || !workspace || !w->router || !w->gate || !w->up || !w->down ||
+                (block && !nw)))
     return fail(MOE_ERR_INVALID, "a required pointer is NULL");
   if (c.has_router_bias && !w->router_bias)
     return fail(MOE_ERR_INVALID, "has_router_bias is set but router_bias is NULL");
   if (c.shared_intermediate > 0 && (!w->shared_gate || !w->shared_up || !w->shared_down))
     return fail(MOE_ERR_INVALID, "shared expert enabled but its weights are NULL");
-  const void* ptrs[] = {x, out, saved, workspace, w->router, w->shared_gate, w->shared_up,
+  const void* ptrs[] = {x, nw, out, saved, workspace, w->router, w->shared_gate, w->shared_up,
                         w->shared_down};
   for (const void* q : ptrs)
     if (q && !aligned16(q)) return fail(MOE_ERR_INVALID, "device pointers must be 16-byte aligned");
@@ -928,34 +999,56 @@ moe_status moe_forward(moe_plan* p, void* stream, int64_t T, const void* x, cons
   }
   const void* const* tabs[3] = {w->gate, w->up, w->down};
   if ((st = upload_tables(p, s, 0, tabs)) != MOE_OK) return st;
-  if (c.dtype == MOE_DTYPE_BF16)
-    return forward_impl<bf16_t>(p, s, T, (const bf16_t*)x, w, (bf16_t*)out, aux_loss, z_loss,
-                                (char*)saved, (char*)workspace);
-  return forward_impl<float>(p, s, T, (const float*)x, w, (float*)out, aux_loss, z_loss,
-                             (char*)saved, (char*)workspace);
+  const bool bf = c.dtype == MOE_DTYPE_BF16;
+  const void* xin = x;
+  const void* resid = nullptr;
+  if (block) {
+    // x = RMSNorm(h): kept in `saved`, or transient in the workspace
+    const bool keep_act = saved && !c.recompute_activations;
+    const WsLayout W = p->ws_layout(T);
+    const SavedLayout LA =
+        keep_act ? p->kept_layout(T) : p->saved_layout(T, moe_plan::Keep::Transient);
+    char* ab = keep_act ? (char*)saved : (char*)workspace + W.infer;
+    char* xn = ab + LA.f[MOE_SAVED_NORM_X];
+    float* rstd = (float*)(ab + LA.f[MOE_SAVED_RSTD]);
+    if (bf) launch_norm_fwd<bf16_t>(p, s, (int)T, x, nw, xn, rstd);
+    else launch_norm_fwd<float>(p, s, (int)T, x, nw, xn, rstd);
+    LAUNCH_CHECK();
+    xin = xn;
+    resid = x;
+  }
+  if (bf)
+    return forward_impl<bf16_t>(p, s, T, (const bf16_t*)xin, w, (bf16_t*)out, aux_loss, z_loss,
+                                (char*)saved, (char*)workspace, (const bf16_t*)resid);
+  return forward_impl<float>(p, s, T, (const float*)xin, w, (float*)out, aux_loss, z_loss,
+                             (char*)saved, (char*)workspace, (const float*)resid);
 }
 
-moe_status moe_backward(moe_plan* p, void* stream, int64_t T, const void* d_out,
-                        const float* d_aux, const float* d_z, const void* x,
-                        const moe_weights* w, const void* saved, void* workspace, void* dx,
-                        const moe_grads* g, uint8_t* has_grad) {
+moe_status backward_entry(moe_plan* p, void* stream, int64_t T, const void* d_out,
+                          const float* d_aux, const float* d_z, const void* x, const void* nw,
+                          const moe_weights* w, const void* saved, void* workspace, void* dx,
+                          void* dnw, const moe_grads* g, uint8_t* has_grad, bool block) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
   if ((st = check_tokens(T)) != MOE_OK) return st;
   if (!w || !g) return fail(MOE_ERR_INVALID, "weights or grads struct is NULL");
   const moe_config& c = p->cfg;
+  if (block && !c.fused_block)
+    return fail(MOE_ERR_INVALID, "moe_block_backward needs a plan created with fused_block = 1");
+  if (!block && c.fused_block)
+    return fail(MOE_ERR_INVALID, "the plan was created with fused_block = 1: call moe_block_backward");
   hipStream_t s = (hipStream_t)stream;
   HIP_TRY(hipSetDevice(p->device));
   if (T == 0) return MOE_OK;  // nothing routed: no gradient is written
   if (!d_out || !x || !saved || !workspace || !dx || !w->router || !w->gate || !w->up ||
-      !w->down || !g->router || !g->gate || !g->up || !g->down)
+      !w->down || !g->router || !g->gate || !g->up || !g->down || (block && (!nw || !dnw)))
     return fail(MOE_ERR_INVALID, "a required pointer is NULL");
   if (c.shared_intermediate > 0 &&
       (!w->shared_gate || !w->shared_up || !w->shared_down || !g->shared_gate || !g->shared_up ||
        !g->shared_down))
     return fail(MOE_ERR_INVALID, "shared expert enabled but its weights or grads are NULL");
-  const void* ptrs[] = {d_out, x, saved, workspace, dx, w->router, g->router, g->shared_gate,
-                        g->shared_up, g->shared_down};
+  const void* ptrs[] = {d_out, x, nw, dnw, saved, workspace, dx, w->router, g->router,
+                        g->shared_gate, g->shared_up, g->shared_down};
   for (const void* q : ptrs)
     if (q && !aligned16(q)) return fail(MOE_ERR_INVALID, "device pointers must be 16-byte aligned");
   const void* const* tabs[3] = {w->gate, w->up, w->down};
@@ -963,11 +1056,76 @@ moe_status moe_backward(moe_plan* p, void* stream, int64_t T, const void* d_out,
   const void* const* gtabs[3] = {(const void* const*)g->gate, (const void* const*)g->up,
                                  (const void* const*)g->down};
   if ((st = upload_tables(p, s, 3, gtabs)) != MOE_OK) return st;
-  if (c.dtype == MOE_DTYPE_BF16)
-    return backward_impl<bf16_t>(p, s, T, (const bf16_t*)d_out, d_aux, d_z, (const bf16_t*)x, w,
-                                 (const char*)saved, (char*)workspace, (bf16_t*)dx, g, has_grad);
-  return backward_impl<float>(p, s, T, (const float*)d_out, d_aux, d_z, (const float*)x, w,
-                              (const char*)saved, (char*)workspace, (float*)dx, g, has_grad);
+  const bool bf = c.dtype == MOE_DTYPE_BF16;
+  const WsLayout W = p->ws_layout(T);
+  const void* xin = x;
+  void* dxo = dx;
+  const float* rstd = nullptr;
+  if (block) {
+    // the layer's input x = RMSNorm(h): kept, or rebuilt with the forward's kernel
+    const bool recompute = c.recompute_activations != 0;
+    const SavedLayout LA =
+        recompute ? p->saved_layout(T, moe_plan::Keep::All) : p->kept_layout(T);
+    char* ab = recompute ? (char*)workspace + W.recomp : (char*)saved;
+    char* xn = ab + LA.f[MOE_SAVED_NORM_X];
+    rstd = (const float*)(ab + LA.f[MOE_SAVED_RSTD]);
+    if (recompute) {
+      if (bf) launch_norm_fwd<bf16_t>(p, s, (int)T, x, nw, xn, (float*)rstd);
+      else launch_norm_fwd<float>(p, s, (int)T, x, nw, xn, (float*)rstd);
+      LAUNCH_CHECK();
+    }
+    xin = xn;
+    dxo = (char*)workspace + W.dxm;
+  }
+  if (bf)
+    st = backward_impl<bf16_t>(p, s, T, (const bf16_t*)d_out, d_aux, d_z, (const bf16_t*)xin, w,
+                               (const char*)saved, (char*)workspace, (bf16_t*)dxo, g, has_grad);
+  else
+    st = backward_impl<float>(p, s, T, (const float*)d_out, d_aux, d_z, (const float*)xin, w,
+                              (const char*)saved, (char*)workspace, (float*)dxo, g, has_grad);
+  if (st != MOE_OK || !block) return st;
+  if (bf)
+    launch_norm_bwd<bf16_t>(p, s, (int)T, (const bf16_t*)dxo, x, nw, rstd, d_out, dx, dnw,
+                            (char*)workspace, W);
+  else
+    launch_norm_bwd<float>(p, s, (int)T, (const float*)dxo, x, nw, rstd, d_out, dx, dnw,
+                           (char*)workspace, W);
+  LAUNCH_CHECK();
+  return MOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+moe_status moe_forward(moe_plan* p, void* stream, int64_t T, const void* x, const moe_weights* w,
+                       void* out, float* aux_loss, float* z_loss, void* saved, void* workspace) {
+  return forward_entry(p, stream, T, x, nullptr, w, out, aux_loss, z_loss, saved, workspace,
+                       false);
+}
+
+moe_status moe_block_forward(moe_plan* p, void* stream, int64_t T, const void* h,
+                             const void* norm_weight, const moe_weights* w, void* out,
+                             float* aux_loss, float* z_loss, void* saved, void* workspace) {
+  return forward_entry(p, stream, T, h, norm_weight, w, out, aux_loss, z_loss, saved, workspace,
+                       true);
+}
+
+moe_status moe_backward(moe_plan* p, void* stream, int64_t T, const void* d_out,
+                        const float* d_aux, const float* d_z, const void* x,
+                        const moe_weights* w, const void* saved, void* workspace, void* dx,
+                        const moe_grads* g, uint8_t* has_grad) {
+  return backward_entry(p, stream, T, d_out, d_aux, d_z, x, nullptr, w, saved, workspace, dx,
+                        nullptr, g, has_grad, false);
+}
+
+moe_status moe_block_backward(moe_plan* p, void* stream, int64_t T, const void* d_out,
+                              const float* d_aux, const float* d_z, const void* h,
+                              const void* norm_weight, const moe_weights* w, const void* saved,
+                              void* workspace, void* dh, void* d_norm_weight, const moe_grads* g,
+                              uint8_t* has_grad) {
+  return backward_entry(p, stream, T, d_out, d_aux, d_z, h, norm_weight, w, saved, workspace,
+                        dh, d_norm_weight, g, has_grad, true);
 }
 
 moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const float* logits,
@@ -993,7 +1151,7 @@ const char* moe_stage_name(int32_t stage) {
   static const char* names[MOE_NUM_STAGES] = {
       "router_gemm", "route", "dispatch", "gather", "gateup_fwd", "down_fwd", "shared_fwd",
       "combine_fwd", "losses", "combine_bwd", "down_dgrad", "down_wgrad", "gateup_dgrad",
-      "gateup_wgrad", "shared_bwd", "router_bwd", "dx", "recompute"};
+      "gateup_wgrad", "shared_bwd", "router_bwd", "dx", "recompute", "norm_fwd", "norm_bwd"};
   if (stage < 0 || stage >= MOE_NUM_STAGES) return "unknown";
   return names[stage];
 }

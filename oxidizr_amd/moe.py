@@ -14,6 +14,7 @@ PyTorch provides device memory and the stream only; the arithmetic runs in
 libmoe_hip.so.
 """
 import ctypes
+import dataclasses
 from dataclasses import dataclass
 from typing import Optional
 
@@ -52,6 +53,12 @@ class MoeConfig:
     # (src/config/activation_checkpointing.rs:25-35): keep only the routing
     # state between forward and backward and recompute the expert activations.
     recompute_activations: bool = False
+    # Block path (moe_block_forward / moe_block_backward): the plan also runs
+    # post_attention_layernorm (RMSNorm, cfg.rms_norm_eps) before the layer and
+    # the residual add after it (src/model.rs:2792-2800). boostr's
+    # default_rms_norm_eps is not pinned by the reference; 1e-6 is the default.
+    fused_block: bool = False
+    rms_norm_eps: float = 1e-6
 
     def has_shared_expert(self) -> bool:
         return True if self.shared_expert_enabled is None else bool(self.shared_expert_enabled)
@@ -108,6 +115,8 @@ class Plan:
         c.aux_switch_coef = cfg.aux_switch_coef
         c.aux_sqprob_coef = cfg.aux_sqprob_coef
         c.recompute_activations = int(cfg.recompute_activations)
+        c.fused_block = int(cfg.fused_block)
+        c.rms_norm_eps = cfg.rms_norm_eps
         self.c = c
         h = ctypes.c_void_p()
         idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
@@ -216,6 +225,39 @@ class Plan:
                                             _p(x2d), ctypes.byref(wstruct), _p(saved), _p(ws),
                                             _p(dx), ctypes.byref(gstruct), _p(has_grad)))
         return dx
+
+    def block_forward(self, h2d, norm_w, wstruct, out=None, saved=None, aux=None, z=None,
+                      need_grad=True):
+        """out = MoE(RMSNorm(h)) + h on a fused_block plan."""
+        T = h2d.shape[0]
+        if out is None:
+            out = torch.empty_like(h2d)
+        if saved is None and need_grad:
+            saved = self.new_saved(T)
+        if aux is None:
+            aux = torch.empty((), dtype=torch.float32, device=self.device)
+        if z is None:
+            z = torch.empty((), dtype=torch.float32, device=self.device)
+        ws = self.workspace(T)
+        _lib.check(_lib.load().moe_block_forward(self.h, self._stream(), T, _p(h2d), _p(norm_w),
+                                                 ctypes.byref(wstruct), _p(out), _p(aux), _p(z),
+                                                 _p(saved), _p(ws)))
+        return out, aux, z, saved
+
+    def block_backward(self, h2d, norm_w, dout, wstruct, gstruct, saved, dh=None, d_norm_w=None,
+                       d_aux=None, d_z=None, has_grad=None):
+        T = h2d.shape[0]
+        if dh is None:
+            dh = torch.empty_like(h2d)
+        if d_norm_w is None:
+            d_norm_w = torch.empty_like(norm_w)
+        ws = self.workspace(T)
+        _lib.check(_lib.load().moe_block_backward(self.h, self._stream(), T, _p(dout), _p(d_aux),
+                                                  _p(d_z), _p(h2d), _p(norm_w),
+                                                  ctypes.byref(wstruct), _p(saved), _p(ws),
+                                                  _p(dh), _p(d_norm_w), ctypes.byref(gstruct),
+                                                  _p(has_grad)))
+        return dh, d_norm_w
 
     def route_from_logits(self, logits, saved=None):
         T = logits.shape[0]
@@ -382,4 +424,102 @@ class MoeLayer(torch.nn.Module):
             return out.reshape(B, S, H), aux, z
         out, aux, z = _MoeFunction.apply(self, x2d, self.router.gate.weight, self.router.bias,
                                          *params)
+        return out.reshape(B, S, H), aux, z
+
+
+class _MoeBlockFunction(torch.autograd.Function):
+    """Autograd node of the MoE sub-block (RMSNorm -> MoE -> residual add)."""
+
+    @staticmethod
+    def forward(ctx, block, h2d, norm_w, router, router_bias, *params):
+        layer = block.ffn
+        E = layer.num_experts
+        gate, up, down = params[0:E], params[E:2 * E], params[2 * E:3 * E]
+        shared = params[3 * E:3 * E + 3] if layer.shared_expert is not None else None
+        plan = layer.plan(h2d)
+        w, keep = plan.weights_struct(router, gate, up, down, router_bias, shared)
+        out, aux, z, saved = plan.block_forward(h2d, norm_w, w)
+        ctx.block, ctx.plan, ctx.saved = block, plan, saved
+        ctx.has_bias = router_bias is not None
+        ctx.save_for_backward(h2d, norm_w, router,
+                              router_bias if router_bias is not None else h2d.new_empty(0), *params)
+        return out, aux, z
+
+    @staticmethod
+    def backward(ctx, dout, daux, dz):
+        layer, plan = ctx.block.ffn, ctx.plan
+        h2d, norm_w, router, router_bias, *params = ctx.saved_tensors
+        if not ctx.has_bias:
+            router_bias = None
+        E = layer.num_experts
+        gate, up, down = params[0:E], params[E:2 * E], params[2 * E:3 * E]
+        shared = params[3 * E:3 * E + 3] if layer.shared_expert is not None else None
+        w, keep_w = plan.weights_struct(router, gate, up, down, router_bias, shared)
+        g_router = torch.empty_like(router)
+        g_bias = torch.empty_like(router_bias) if router_bias is not None else None
+        g_gate = [torch.empty_like(t) for t in gate]
+        g_up = [torch.empty_like(t) for t in up]
+        g_down = [torch.empty_like(t) for t in down]
+        g_shared = [torch.empty_like(t) for t in shared] if shared is not None else None
+        g, keep_g = plan.grads_struct(g_router, g_gate, g_up, g_down, g_bias, g_shared)
+        has_grad = torch.empty(E, dtype=torch.uint8, device=h2d.device)
+        dout = dout.contiguous() if dout is not None else torch.zeros_like(h2d)
+        daux = (daux if daux is not None else torch.zeros((), device=h2d.device)).float().contiguous()
+        dz = (dz if dz is not None else torch.zeros((), device=h2d.device)).float().contiguous()
+        dh, d_norm_w = plan.block_backward(h2d, norm_w, dout, w, g, ctx.saved, d_aux=daux, d_z=dz,
+                                           has_grad=has_grad)
+        hg = has_grad.cpu().tolist()
+        ctx.saved = None
+
+        def keep(lst):
+            return [t if hg[e] else None for e, t in enumerate(lst)]
+        grads = keep(g_gate) + keep(g_up) + keep(g_down)
+        if g_shared is not None:
+            grads += g_shared
+        return (None, dh, d_norm_w, g_router, g_bias, *grads)
+
+
+class MoeBlock(torch.nn.Module):
+    """The MoE sub-block of a decoder block (src/model.rs:2792-2800):
+    forward(h [B, S, H]) -> (MoE(post_attention_layernorm(h)) + h, aux, z),
+    run as one fused_block plan."""
+
+    def __init__(self, cfg: MoeConfig, dtype=torch.bfloat16, device="cuda"):
+        super().__init__()
+        cfg = dataclasses.replace(cfg, fused_block=True)
+        self.post_attention_layernorm = torch.nn.Module()
+        self.post_attention_layernorm.weight = torch.nn.Parameter(
+            torch.ones(cfg.hidden_size, dtype=dtype, device=device))
+        self.ffn = MoeLayer(cfg, dtype=dtype, device=device)
+
+    def trainable_parameters(self):
+        return ([("post_attention_layernorm.weight", self.post_attention_layernorm.weight)] +
+                self.ffn.trainable_parameters())
+
+    def forward(self, h):
+        if h.dim() != 3:
+            raise ModelError(f"MoE expects [B, Seq, Hidden], got {list(h.shape)}")
+        B, S, H = h.shape
+        h2d = h.reshape(B * S, H).contiguous()
+        layer = self.ffn
+        params = ([e.gate_proj.weight for e in layer.experts] +
+                  [e.up_proj.weight for e in layer.experts] +
+                  [e.down_proj.weight for e in layer.experts])
+        if layer.shared_expert is not None:
+            params += [layer.shared_expert.gate_proj.weight, layer.shared_expert.up_proj.weight,
+                       layer.shared_expert.down_proj.weight]
+        norm_w = self.post_attention_layernorm.weight
+        tracked = [h2d, norm_w, layer.router.gate.weight] + params
+        if layer.router.bias is not None:
+            tracked.append(layer.router.bias)
+        if not (torch.is_grad_enabled() and any(t.requires_grad for t in tracked)):
+            plan = layer.plan(h2d)
+            E = layer.num_experts
+            shared = params[3 * E:] if layer.shared_expert is not None else None
+            w, keep = plan.weights_struct(layer.router.gate.weight, params[0:E], params[E:2 * E],
+                                          params[2 * E:3 * E], layer.router.bias, shared)
+            out, aux, z, _ = plan.block_forward(h2d, norm_w, w, need_grad=False)
+            return out.reshape(B, S, H), aux, z
+        out, aux, z = _MoeBlockFunction.apply(self, h2d, norm_w, layer.router.gate.weight,
+                                              layer.router.bias, *params)
         return out.reshape(B, S, H), aux, z

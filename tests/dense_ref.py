@@ -17,10 +17,24 @@ import torch.nn.functional as F
 def dense_moe(p, cfg, need_grad=True, d_aux=0.0, d_z=0.0):
     """p: dict of numpy inputs (see oxidizr_amd.synth.host_problem). Returns
     (out, aux, z, grads or None, routing dict)."""
-    T, H, E, k, I, S = cfg.T, cfg.H, cfg.E, cfg.k, cfg.I, cfg.S
     t = {n: torch.tensor(np.asarray(v, np.float64), requires_grad=need_grad and n != "dout")
          for n, v in p.items()}
-    x = t["x"]
+    return _dense(t, t["x"], cfg, need_grad, d_aux, d_z, None)
+
+
+def dense_block(p, cfg, eps, need_grad=True, d_aux=0.0, d_z=0.0):
+    """The MoE sub-block of a decoder block (reference src/model.rs:2792-2800):
+    out = MoE(rms_norm(h)) + h, with torch's own F.rms_norm. p holds "h" and
+    "norm_weight" in place of "x"; the grads dict then has "h" and
+    "norm_weight"."""
+    t = {n: torch.tensor(np.asarray(v, np.float64), requires_grad=need_grad and n != "dout")
+         for n, v in p.items()}
+    x = F.rms_norm(t["h"], (cfg.H,), t["norm_weight"], eps)
+    return _dense(t, x, cfg, need_grad, d_aux, d_z, t["h"])
+
+
+def _dense(t, x, cfg, need_grad, d_aux, d_z, resid):
+    T, H, E, k, I, S = cfg.T, cfg.H, cfg.E, cfg.k, cfg.I, cfg.S
     logits = x @ t["router"].T
     if cfg.has_bias:
         logits = logits + t["router_bias"]
@@ -40,6 +54,8 @@ def dense_moe(p, cfg, need_grad=True, d_aux=0.0, d_z=0.0):
         ys = F.linear(F.silu(F.linear(x, t["shared_gate"])) * F.linear(x, t["shared_up"]),
                       t["shared_down"])
         out = out + cfg.shared_scale * ys
+    if resid is not None:
+        out = out + resid
     counts = torch.bincount(order.flatten(), minlength=E).to(torch.float64)
     f = counts / (T * k)
     P = probs.mean(dim=0)

@@ -1,5 +1,7 @@
 """Shared helpers of the GPU parity tests: seeded inputs, one GPU forward +
 backward through the C ABI, and the same pass on the CPU oracle."""
+import dataclasses
+
 import numpy as np
 import torch
 
@@ -111,3 +113,46 @@ def oracle_run(case, logits, d_aux=0.0, d_z=0.0, backward=True, dout=None, x=Non
     if backward:
         res.update(o.backward(p["dout"], d_aux=d_aux, d_z=d_z))
     return res
+
+
+def rounded(a, tdtype):
+    """a as the device dtype sees it (float64 numpy)."""
+    return torch.tensor(np.asarray(a, np.float64)).to(tdtype).double().numpy()
+
+
+def gpu_block_run(case, h, norm_w, eps, d_aux=0.0, d_z=0.0, recompute=False):
+    """moe_block_forward + moe_block_backward on cuda:0 (fused_block plan)."""
+    dev = torch.device("cuda:0")
+    p = case.p
+    dt = case.tdtype
+    t = {n: torch.tensor(v, device=dev).to(dt) for n, v in p.items() if n != "router_bias"}
+    ht = torch.tensor(h, device=dev).to(dt)
+    nw = torch.tensor(norm_w, device=dev).to(dt)
+    bias = torch.tensor(p["router_bias"], device=dev) if case.bias is not None else None
+    T = ht.shape[0]
+    cfg = dataclasses.replace(case.cfg, fused_block=True, rms_norm_eps=eps,
+                              recompute_activations=recompute)
+    plan = Plan(cfg, dt, dev)
+    gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
+    shared = (t["shared_gate"], t["shared_up"], t["shared_down"]) if case.S else None
+    w, _keep = plan.weights_struct(t["router"], gate, up, down, bias, shared)
+    out, aux, z, saved = plan.block_forward(ht, nw, w)
+    res = {"out": out, "aux": aux, "z": z, "logits": plan.saved_field(saved, T, "logits")}
+    g_router = torch.empty_like(t["router"])
+    g_gate = [torch.full_like(a, float("nan")) for a in gate]
+    g_up = [torch.full_like(a, float("nan")) for a in up]
+    g_down = [torch.full_like(a, float("nan")) for a in down]
+    g_sh = [torch.empty_like(a) for a in shared] if shared else None
+    g, _keep2 = plan.grads_struct(g_router, g_gate, g_up, g_down, None, g_sh)
+    has_grad = torch.full((case.E,), 7, dtype=torch.uint8, device=dev)
+    da = torch.tensor(float(d_aux), device=dev)
+    dz = torch.tensor(float(d_z), device=dev)
+    dh, dnw = plan.block_backward(ht, nw, t["dout"], w, g, saved, d_aux=da, d_z=dz,
+                                  has_grad=has_grad)
+    res.update({"dh": dh, "norm_weight": dnw, "router": g_router, "gate": torch.stack(g_gate),
+                "up": torch.stack(g_up), "down": torch.stack(g_down), "has_grad": has_grad})
+    if g_sh:
+        res.update({"shared_gate": g_sh[0], "shared_up": g_sh[1], "shared_down": g_sh[2]})
+    torch.cuda.synchronize()
+    return {n: (v.float().cpu().numpy() if isinstance(v, torch.Tensor) else v)
+            for n, v in res.items()}

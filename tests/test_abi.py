@@ -68,9 +68,10 @@ def test_config_defaults_and_names():
     assert c.router_temperature == 1.0 and c.shared_expert_scale == 1.0
     assert c.aux_switch_coef == 1.0 and c.aux_sqprob_coef == 1.0
     assert c.norm_topk_prob == 0 and c.has_router_bias == 0
-    assert c.recompute_activations == 0
+    assert c.recompute_activations == 0 and c.fused_block == 0
     names = [L.moe_stage_name(i).decode() for i in range(_lib.NUM_STAGES)]
-    assert names[0] == "router_gemm" and names[-2:] == ["dx", "recompute"]
+    assert names[0] == "router_gemm" and names[-4:] == ["dx", "recompute", "norm_fwd", "norm_bwd"]
+    assert len(set(names)) == len(names)
     assert L.moe_stage_name(_lib.NUM_STAGES).decode() == "unknown"
     assert b"gfx950" in L.moe_version()
 

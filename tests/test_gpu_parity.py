@@ -16,7 +16,7 @@ import torch
 from oracle import moe_oracle as mo
 from oxidizr_amd.moe import MoeConfig, MoeLayer, Plan
 from oxidizr_amd.synth import zipf_bias
-from tests.gpu_helpers import Case, gpu_run, oracle_run, rel
+from tests.gpu_helpers import Case, gpu_block_run, gpu_run, oracle_run, rel, rounded
 
 pytestmark = pytest.mark.gpu
 
@@ -284,3 +284,64 @@ def test_recompute_shrinks_saved_state():
     assert keep.saved_bytes(T) - rec.saved_bytes(T) >= act
     assert rec.saved_bytes(T) < 40 * T * 16
     assert rec.workspace_bytes(T) > keep.workspace_bytes(T)
+
+
+# ---------------------------------------------------------------- block path (RMSNorm + residual)
+
+BLOCK_CASES = [("f32", 300, 1e-5), ("bf16", 300, 1e-2), ("bf16", 40, 1e-2)]
+
+
+@pytest.mark.parametrize("dtype,T,tol", BLOCK_CASES)
+def test_block_forward_backward_parity(dtype, T, tol):
+    # moe_block_forward / moe_block_backward against the block oracle
+    # (RMSNorm -> layer -> residual add, float64), routed from the GPU's logits
+    case = Case(T=T, H=128, E=16, k=2, I=64, S=64, dtype=dtype, w_std=0.05, seed=21)
+    rng = np.random.default_rng(21)
+    h = rounded(2.0 * rng.standard_normal((T, 128)), case.tdtype)
+    nw = rounded(1.0 + 0.2 * rng.standard_normal(128), case.tdtype)
+    eps = 1e-5
+    g = gpu_block_run(case, h, nw, eps, d_aux=0.01, d_z=0.001)
+    p = case.p
+    o = mo.MoeBlockOracle(case.ocfg, eps)
+    out, aux, z = o.forward(h, nw, p["router"], p["gate"], p["up"], p["down"], None,
+                            p["shared_gate"], p["shared_up"], p["shared_down"],
+                            logits_in=g["logits"])
+    og = o.backward(p["dout"], d_aux=0.01, d_z=0.001)
+    np.testing.assert_array_equal(g["has_grad"], og["has_grad"])
+    hg = og["has_grad"].astype(bool)
+    errs = {"out": rel(g["out"], out), "dh": rel(g["dh"], og["h"]),
+            "d_norm_weight": rel(g["norm_weight"], og["norm_weight"]),
+            "d_router": rel(g["router"], og["router"]),
+            "aux": abs(float(g["aux"]) - aux) / abs(aux), "z": abs(float(g["z"]) - z) / abs(z)}
+    for n in ("gate", "up", "down"):
+        errs["d_" + n] = rel(g[n][hg], og[n][hg])
+    for n in ("shared_gate", "shared_up", "shared_down"):
+        errs["d_" + n] = rel(g[n], og[n])
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"over tolerance {tol}: {bad} (all: {errs})"
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_block_recompute_is_bitwise_equal(dtype):
+    case = Case(T=200, H=128, E=8, k=2, I=64, S=64, dtype=dtype, w_std=0.05, seed=23)
+    rng = np.random.default_rng(23)
+    h = rounded(rng.standard_normal((200, 128)), case.tdtype)
+    nw = rounded(1.0 + 0.2 * rng.standard_normal(128), case.tdtype)
+    a = gpu_block_run(case, h, nw, 1e-6, d_aux=0.01)
+    b = gpu_block_run(case, h, nw, 1e-6, d_aux=0.01, recompute=True)
+    for n in ("out", "aux", "z", "dh", "norm_weight", "router", "gate", "up", "down",
+              "shared_gate", "shared_up", "shared_down"):
+        np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+
+
+def test_block_plan_rejects_plain_entry_points():
+    dev = torch.device("cuda:0")
+    cfg = MoeConfig(hidden_size=64, num_experts=4, experts_per_tok=2, intermediate_size=32,
+                    fused_block=True)
+    plan = Plan(cfg, torch.float32, dev)
+    x = torch.zeros(8, 64, device=dev)
+    gate = [torch.zeros(32, 64, device=dev) for _ in range(4)]
+    down = [torch.zeros(64, 32, device=dev) for _ in range(4)]
+    w, _k = plan.weights_struct(torch.zeros(4, 64, device=dev), gate, gate, down)
+    with pytest.raises(Exception, match="fused_block"):
+        plan.forward(x, w)

@@ -17,11 +17,12 @@ is therefore pinned by checks that a plausible mistake would fail:
 """
 import numpy as np
 import pytest
+import torch
 from scipy.special import logsumexp, softmax
 
 from oracle import moe_oracle as mo
 from oxidizr_amd.synth import host_problem, zipf_bias
-from tests.dense_ref import dense_moe
+from tests.dense_ref import dense_block, dense_moe
 
 pytestmark = pytest.mark.filterwarnings("ignore::RuntimeWarning")
 
@@ -263,3 +264,46 @@ def test_oracle_is_deterministic():
     ga, gb = a.backward(p["dout"], 0.1, 0.1), b.backward(p["dout"], 0.1, 0.1)
     for n in ("x", "router", "gate", "shared_down"):
         np.testing.assert_array_equal(ga[n], gb[n])
+
+
+# ---------------------------------------------------------------- block path
+
+def test_rmsnorm_matches_torch_rms_norm_and_closed_forms():
+    rng = np.random.default_rng(5)
+    h = rng.standard_normal((7, 24))
+    w = rng.standard_normal(24)
+    x, rstd = mo.rmsnorm_forward(h, w, 1e-6)
+    want = torch.nn.functional.rms_norm(torch.tensor(h), (24,), torch.tensor(w), 1e-6).numpy()
+    assert _rel(x, want) < 1e-14
+    # a constant row c normalises to sign(c) * w (up to eps); scaling a row
+    # leaves the result unchanged; eps enters under the square root
+    c = np.full((1, 24), -3.0)
+    xc, rc = mo.rmsnorm_forward(c, w, 0.0)
+    assert _rel(xc[0], -w) < 1e-15 and abs(rc[0] - 1 / 3.0) < 1e-15
+    x5, _ = mo.rmsnorm_forward(5.0 * h, w, 0.0)
+    x1, _ = mo.rmsnorm_forward(h, w, 0.0)
+    assert _rel(x5, x1) < 1e-14
+    _, r_eps = mo.rmsnorm_forward(c, w, 7.0)
+    assert abs(r_eps[0] - 1 / 4.0) < 1e-15
+
+
+@pytest.mark.parametrize("case", CASES[:2])
+def test_block_forward_backward_match_autograd(case):
+    cfg = mo.make_cfg(**case)
+    p = _problem(cfg, seed=3)
+    rng = np.random.default_rng(9)
+    pb = dict(p)
+    pb["h"] = pb.pop("x") * 3.0
+    pb["norm_weight"] = 1.0 + 0.3 * rng.standard_normal(cfg.H)
+    eps = 1e-5
+    o = mo.MoeBlockOracle(cfg, eps)
+    out, aux, z = o.forward(pb["h"], pb["norm_weight"], pb["router"], pb["gate"], pb["up"],
+                            pb["down"], None, pb.get("shared_gate"), pb.get("shared_up"),
+                            pb.get("shared_down"))
+    g = o.backward(pb["dout"], d_aux=0.37, d_z=0.11)
+    want_out, want_aux, want_z, want, _ = dense_block(pb, cfg, eps, d_aux=0.37, d_z=0.11)
+    assert _rel(out, want_out) < 1e-12
+    assert abs(aux - want_aux) < 1e-12 and abs(z - want_z) < 1e-12
+    assert _rel(g["h"], want["h"]) < 1e-11
+    assert _rel(g["norm_weight"], want["norm_weight"]) < 1e-11
+    assert _rel(g["router"], want["router"]) < 1e-11
