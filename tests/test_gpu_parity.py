@@ -345,3 +345,30 @@ def test_block_plan_rejects_plain_entry_points():
     w, _k = plan.weights_struct(torch.zeros(4, 64, device=dev), gate, gate, down)
     with pytest.raises(Exception, match="fused_block"):
         plan.forward(x, w)
+
+
+# ---------------------------------------------------------------- packed experts from a checkpoint
+
+def test_layer_from_packed_checkpoint_matches(tmp_path):
+    # weights saved under the checkpoint names, loaded into packed [E, I, H]
+    # storage on the GPU: the plan reads the packed tensors in place and gives
+    # the same bits as the same weights held in memory
+    from oxidizr_amd.checkpoint import PackedExperts, load_packed, save_packed
+    case = Case(T=200, H=128, E=8, k=2, I=64, S=64, dtype="bf16", w_std=0.05, seed=31)
+    p = case.p
+    src = PackedExperts(*(torch.tensor(p[n]).to(torch.bfloat16)
+                          for n in ("router", "gate", "up", "down")),
+                        shared=tuple(torch.tensor(p[n]).to(torch.bfloat16)
+                                     for n in ("shared_gate", "shared_up", "shared_down")))
+    path = str(tmp_path / "moe.safetensors")
+    save_packed(path, 0, src)
+    dev = torch.device("cuda:0")
+    pk = load_packed(path, 0, 128, 8, 64, 64, device=dev)
+    plan = Plan(case.cfg, torch.bfloat16, dev)
+    w, _keep = pk.weights_struct(plan)
+    x = torch.tensor(p["x"], device=dev).to(torch.bfloat16)
+    out, aux, z, _ = plan.forward(x, w)
+    torch.cuda.synchronize()
+    ref = gpu_run(case, backward=False)
+    np.testing.assert_array_equal(out.float().cpu().numpy(), ref["out"])
+    assert float(aux) == float(ref["aux"])
