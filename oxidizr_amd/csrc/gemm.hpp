@@ -214,11 +214,15 @@ MOE_DEV int tr_swz(int k) { return (k & 3) << 2; }
 
 template <class C, typename T, int R>
 struct DmaStager {
-  static constexpr int KV = C::BK / C::V;  // 16-byte slots per row
-  static_assert(KV == 8, "one 1 KB LDS chunk = 8 rows of 8 slots");
-  static_assert(R % 32 == 0, "4 waves x 8 rows per instruction");
-  static constexpr int PER = R / 32;       // instructions per wave per k-tile
-  rsrc_t rs[2];                            // one per K segment
+  static constexpr int KV = C::BK / C::V;    // 16-byte slots per row
+  static_assert(KV == 8 || KV == 4, "rows of 8 or 4 slots");
+  static constexpr int RPI = 64 / KV;        // rows per wave per 1 KB instruction
+  static_assert(R % (4 * RPI) == 0, "4 waves x RPI rows per instruction");
+  static constexpr int PER = R / (4 * RPI);  // instructions per wave per k-tile
+  // slot swizzle: the 16 lanes of a ds_read_b128 phase read 16 rows at one kv
+  // and must hit 16 distinct 16-byte bank groups of a 256-byte window
+  MOE_DEV static int swz(int r) { return KV == 8 ? nt_swz(r) : ((r >> 2) & 3); }
+  rsrc_t rs[2];                              // one per K segment
   int k_valid[2];
   uint32_t voff, step;
   int kcol;
@@ -230,10 +234,10 @@ struct DmaStager {
     rs[0] = rs[1] = rsrc_of(d);
     k_valid[0] = k_valid[1] = d.k_valid;
     const int lane = tid & 63, wave = tid >> 6;
-    const int row = wave * 8 + (lane >> 3);   // bits 0-3 are the same for every chunk i
-    kcol = ((lane & 7) ^ nt_swz(row)) * C::V;
+    const int row = wave * RPI + lane / KV;   // the swizzle bits are the same for every chunk i
+    kcol = ((lane % KV) ^ swz(row)) * C::V;
     voff = (uint32_t)((row * d.ld + kcol) * (int64_t)sizeof(T));
-    step = (uint32_t)(32 * d.ld * (int64_t)sizeof(T));
+    step = (uint32_t)(4 * RPI * d.ld * (int64_t)sizeof(T));
   }
   MOE_DEV void init_second(const OpDesc<T>& d) {  // same ld and rows as the first
     rs[1] = rsrc_of(d);
@@ -246,11 +250,11 @@ struct DmaStager {
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs[seg], (lds_void_t*)(tile + (i * 32 + wave * 8) * C::BK), 16,
+          rs[seg], (lds_void_t*)(tile + (i * 4 * RPI + wave * RPI) * C::BK), 16,
           kin ? voff + i * step : kOobOffset, soff, 0, 0);
   }
   MOE_DEV static u32x4 frag(const T* tile, int row, int kv) {
-    return *reinterpret_cast<const u32x4*>(tile + row * C::BK + ((kv ^ nt_swz(row)) * C::V));
+    return *reinterpret_cast<const u32x4*>(tile + row * C::BK + ((kv ^ swz(row)) * C::V));
   }
 };
 
@@ -566,6 +570,15 @@ MOE_DEV void for_each_frag(const f32x16 (&acc)[NACC][C::TN][C::TM], F&& f) {
 // accumulators, rows padded to 36 floats.
 template <class C, int NACC>
 constexpr int epi_lds_floats() { return 4 * NACC * C::WM * 36; }
+
+// LDS elements of a kernel whose main loop (NA A / NB B operands) is followed
+// by the row epilogue over NACC accumulator sets in the same buffer.
+template <class C, typename T, int NA, int NB, int NACC>
+constexpr int kernel_smem_elems() {
+  constexpr int a = smem_elems<C, NA, NB>();
+  constexpr int b = (epi_lds_floats<C, NACC>() * 4 + (int)sizeof(T) - 1) / (int)sizeof(T);
+  return a > b ? a : b;
+}
 
 // Row epilogue: calls f(m_local, n_local, v, q) with v[x][i] = acc[x] at
 // (m_local, n_local + i) for i < 8, n_local a multiple of 8.  The accumulators

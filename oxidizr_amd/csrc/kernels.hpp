@@ -634,7 +634,7 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
                                                     const T* __restrict__ U,
                                                     T* __restrict__ dG, T* __restrict__ dU) {
   using C = typename Tilings<T>::Big;
-  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);  // [H, N]: element (n, k=h) at wd + h*N + n
