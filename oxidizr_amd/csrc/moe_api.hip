@@ -88,6 +88,7 @@ struct SplitPlan {
 };
 template <class C>
 SplitPlan plan_split(int M, int N, int K) {
+  if (K <= 0) return {1, C::BK};  // no tokens: nothing to split
   const int tiles = ceil_div(M, C::BM) * ceil_div(N, C::BN);
   const int nkt = ceil_div(K, C::BK);
   const int most = K / (4 * C::BK) > 1 ? K / (4 * C::BK) : 1;
