@@ -408,26 +408,31 @@ __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_his
 
 
 // Stable scatter: position of assignment (t, j) = offset of its expert +
-// number of earlier tokens (same expert) before it.  Ranks inside a wave come
-// from ballots that match expert ids bit by bit; across the block's 4 waves
-// from per-wave counts.
+// number of earlier tokens (same expert) before it.  Inside a wave, the lanes
+// that chose expert e are the bits of a 64-lane mask built with LDS atomic
+// ORs (order-independent), so a lane's rank is a popcount of the mask below
+// it; across the block's 4 waves the offsets come from per-wave counts.  A
+// token picks distinct experts, so each lane is in a mask at most once.
 __global__ __launch_bounds__(256) void k_scatter(const int* __restrict__ idx, int Tn, int k,
-                                                 int E, int nbits,
-                                                 const int* __restrict__ block_base,
+                                                 int E, const int* __restrict__ block_base,
                                                  int* __restrict__ perm,
                                                  int* __restrict__ inv_perm) {
   extern __shared__ int lds[];
-  int* wcnt = lds;            // [4][E]
-  int* wbase = lds + 4 * E;   // [4][E]
+  int* wcnt = lds;                                // [4][E]
+  int* wbase = lds + 4 * E;                       // [4][E]
+  unsigned* wmask = (unsigned*)(lds + 8 * E);     // [4][E][2] lane masks
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int t = blockIdx.x * 256 + tid;
   const bool valid = t < Tn;
-  for (int i = tid; i < 4 * E; i += 256) wcnt[i] = 0;
+  for (int i = tid; i < 16 * E; i += 256) lds[i] = 0;
   __syncthreads();
   int keys[16];
   for (int j = 0; j < k; ++j) {
-    keys[j] = valid ? idx[(int64_t)t * k + j] : E;
-    if (valid) atomicAdd(&wcnt[wave * E + keys[j]], 1);
+    keys[j] = valid ? idx[(int64_t)t * k + j] : 0;
+    if (valid) {
+      atomicAdd(&wcnt[wave * E + keys[j]], 1);
+      atomicOr(&wmask[(wave * E + keys[j]) * 2 + (lane >> 5)], 1u << (lane & 31));
+    }
   }
   __syncthreads();
   for (int e = tid; e < E; e += 256) {
@@ -438,24 +443,15 @@ __global__ __launch_bounds__(256) void k_scatter(const int* __restrict__ idx, in
     }
   }
   __syncthreads();
-  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  if (!valid) return;
+  const unsigned below = (1u << (lane & 31)) - 1u;
   for (int j = 0; j < k; ++j) {
     const int e = keys[j];
-    uint64_t uni = 0;
-    for (int j2 = 0; j2 < k; ++j2) {
-      uint64_t m = ~0ull;
-      for (int bit = 0; bit < nbits; ++bit) {
-        const uint64_t bal = __ballot((keys[j2] >> bit) & 1);
-        m &= ((e >> bit) & 1) ? bal : ~bal;
-      }
-      uni |= m;
-    }
-    const int rank = __popcll(uni & below);
-    if (valid) {
-      const int pos = block_base[(int64_t)blockIdx.x * E + e] + wbase[wave * E + e] + rank;
-      perm[pos] = t * k + j;
-      inv_perm[(int64_t)t * k + j] = pos;
-    }
+    const unsigned lo = wmask[(wave * E + e) * 2], hi = wmask[(wave * E + e) * 2 + 1];
+    const int rank = lane < 32 ? __popc(lo & below) : __popc(lo) + __popc(hi & below);
+    const int pos = block_base[(int64_t)blockIdx.x * E + e] + wbase[wave * E + e] + rank;
+    perm[pos] = t * k + j;
+    inv_perm[(int64_t)t * k + j] = pos;
   }
 }
 
@@ -538,7 +534,10 @@ __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGr
 
 // ------------------------------------------------------------------ combine
 // out[t] = sum_j w[t, j] * Y[inv_perm[t, j]] (+ s * Ys[t]) (+ resid[t]), added in
-// that order in fp32 and rounded once; one wave per token.
+// that order in fp32 and rounded once.  One wave per (token, slice of 64
+// 16-byte vectors of the row); the k expert rows of a slice are all requested
+// before the first one is added.
+constexpr int kCombineSlice = 64;  // 16-byte vectors per wave
 template <typename T>
 __global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
                                                      const int* __restrict__ inv_perm,
@@ -547,38 +546,50 @@ __global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
                                                      int k, int H, const T* __restrict__ resid,
                                                      T* __restrict__ out) {
   constexpr int V = Vec16<T>::N;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= Tn) return;
-  const int lane = threadIdx.x & 63;
+  const int nv = H / V;
+  const int nsl = (nv + kCombineSlice - 1) / kCombineSlice;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (wid >= (int64_t)Tn * nsl) return;
+  const int t = (int)(wid / nsl), sl = (int)(wid % nsl);
+  const int c = sl * kCombineSlice + (threadIdx.x & 63);
+  if (c >= nv) return;
   const int64_t TK = (int64_t)Tn * k;
-  int64_t pos[16];
+  u32x4 ya[16];
   float wj[16];
-  for (int j = 0; j < k; ++j) {
-    int64_t p = inv_perm[(int64_t)t * k + j];
-    pos[j] = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
-    wj[j] = w[(int64_t)t * k + j];
-  }
-  for (int c = lane; c < H / V; c += 64) {
-    float acc[V], y[V];
 #pragma unroll
-    for (int i = 0; i < V; ++i) acc[i] = 0.0f;
-    for (int j = 0; j < k; ++j) {
-      unpack16(ld16(Y + pos[j] * H + c * V), y, T());
+  for (int j = 0; j < 16; ++j) {
+    if (j < k) {
+      int64_t p = inv_perm[(int64_t)t * k + j];
+      p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+      wj[j] = w[(int64_t)t * k + j];
+      ya[j] = ld16(Y + p * H + c * V);
+    }
+  }
+  u32x4 ys{}, rs{};
+  if (Ys) ys = ld16(Ys + (int64_t)t * H + c * V);
+  if (resid) rs = ld16(resid + (int64_t)t * H + c * V);
+  float acc[V], y[V];
+#pragma unroll
+  for (int i = 0; i < V; ++i) acc[i] = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    if (j < k) {
+      unpack16(ya[j], y, T());
 #pragma unroll
       for (int i = 0; i < V; ++i) acc[i] += wj[j] * y[i];
     }
-    if (Ys) {
-      unpack16(ld16(Ys + (int64_t)t * H + c * V), y, T());
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += s * y[i];
-    }
-    if (resid) {  // the block's residual add, fused
-      unpack16(ld16(resid + (int64_t)t * H + c * V), y, T());
-#pragma unroll
-      for (int i = 0; i < V; ++i) acc[i] += y[i];
-    }
-    st16(out + (int64_t)t * H + c * V, pack16(acc, T()));
   }
+  if (Ys) {
+    unpack16(ys, y, T());
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] += s * y[i];
+  }
+  if (resid) {  // the block's residual add, fused
+    unpack16(rs, y, T());
+#pragma unroll
+    for (int i = 0; i < V; ++i) acc[i] += y[i];
+  }
+  st16(out + (int64_t)t * H + c * V, pack16(acc, T()));
 }
 
 // dw[t, j] = <dout[t], Y[pos]>,  dY[pos] = w[t, j] * dout[t].
@@ -1072,11 +1083,16 @@ MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b) {
 
 // WIDE = false handles the experts with at most 16 tokens (one chunk of token
 // rows), WIDE = true those with 17..64; both are launched and each skips the
-// other's experts.  GATEUP: a workgroup covers 32 intermediate columns; waves 0
-// and 1 stream 16 gate rows each, waves 2 and 3 the matching up rows (one
-// matrix per wave keeps registers low, so more waves keep loads in flight),
-// and the gate accumulators reach the up waves through LDS for the SwiGLU
-// epilogue.  Otherwise (down projection) each of the 4 waves owns 16 rows.
+// other's experts.  Each wave streams 16 * NR weight rows, so every token
+// fragment it loads feeds NR MFMAs.  GATEUP: waves 0 and 1 stream gate rows,
+// waves 2 and 3 the matching up rows (one matrix per wave keeps registers low,
+// so more waves keep loads in flight), and the gate accumulators reach the up
+// waves through LDS for the SwiGLU epilogue; a workgroup covers 32 * NR
+// intermediate columns.  Otherwise (down projection) each of the 4 waves owns
+// 16 * NR rows.
+// One 16-row block per wave: two gave the same bandwidth on the config-4
+// shape, four lowered occupancy to 2 waves per SIMD and lost 9 %.
+constexpr int kSkinnyNR = 1;
 template <bool GATEUP, bool WIDE>
 __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X,
                                                     const int* __restrict__ offsets, int Mdense,
@@ -1085,9 +1101,10 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
                                                     int K, int N, bf16_t* __restrict__ out0,
                                                     bf16_t* __restrict__ out1,
                                                     bf16_t* __restrict__ out2) {
-  constexpr int ROWS_PER_WG = GATEUP ? 32 : 64;
+  constexpr int NR = kSkinnyNR;
+  constexpr int ROWS_PER_WG = (GATEUP ? 32 : 64) * NR;
   constexpr int NC = WIDE ? 4 : 1;
-  __shared__ f32x4 gbuf[GATEUP ? 2 : 1][NC][64];
+  __shared__ f32x4 gbuf[GATEUP ? 2 : 1][NR][NC][64];
   const int nNb = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
   const int e = uni(blockIdx.x / nNb), nb = uni(blockIdx.x % nNb);
   const int r0 = offsets ? offsets[e] : 0;
@@ -1095,9 +1112,9 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
   if (M <= 0 || (WIDE ? M <= 16 : M > 16)) return;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int mat = GATEUP ? wave >> 1 : 0;                 // 0: W0 (gate / down), 1: W1 (up)
-  const int n0 = nb * ROWS_PER_WG + (GATEUP ? (wave & 1) : wave) * 16;
+  const int n0 = nb * ROWS_PER_WG + (GATEUP ? (wave & 1) : wave) * 16 * NR;
   const int g = lane >> 4, rl = lane & 15;
-  const int nrows = max(0, min(16, N - n0));
+  const int nrows = max(0, min(16 * NR, N - n0));
   const bool active = nrows > 0;                           // wave-uniform
   const bf16_t* wsrc = mat ? pick(w1_tab, w1_one, e) : pick(w0_tab, w0_one, e);
   const rsrc_t rw = make_rsrc(wsrc + (int64_t)(active ? n0 : 0) * K,
@@ -1105,17 +1122,22 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
   const rsrc_t rx = make_rsrc(X + (int64_t)r0 * K, (uint32_t)((int64_t)M * K * 2));
   const int nch = (M + 15) / 16;
   const uint32_t vw = (uint32_t)((rl * K + 8 * g) * 2);
-  f32x4 acc[NC];
+  const uint32_t sub = (uint32_t)(16 * K * 2);            // bytes between 16-row blocks
+  f32x4 acc[NR][NC];
 #pragma unroll
-  for (int c = 0; c < NC; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int sr = 0; sr < NR; ++sr)
+#pragma unroll
+    for (int c = 0; c < NC; ++c) acc[sr][c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   if (active) {
     for (int kc = 0; kc * 256 < K; ++kc) {
       const uint32_t soff = (uint32_t)kc * 512;
-      u32x4 wa[8];
+      u32x4 wa[NR][8];
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const bool kin = kc * 256 + 32 * q + 8 * g < K;
-        wa[q] = buf_ld16(rw, kin ? vw + 64 * q : kOobOffset, soff);
+#pragma unroll
+        for (int sr = 0; sr < NR; ++sr)
+          wa[sr][q] = buf_ld16(rw, kin ? vw + sr * sub + 64 * q : kOobOffset, soff);
       }
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
@@ -1128,40 +1150,48 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
           xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
         }
 #pragma unroll
-        for (int q = 0; q < 8; ++q) mfma16(acc[c], xa[q], wa[q]);
+        for (int q = 0; q < 8; ++q)
+#pragma unroll
+          for (int sr = 0; sr < NR; ++sr) mfma16(acc[sr][c], xa[q], wa[sr][q]);
       }
     }
   }
-  // lane holds D[token = 16 c + 4 g + r][row = rl]
+  // lane holds D[token = 16 c + 4 g + r][row = 16 sr + rl]
   if constexpr (GATEUP) {
     if (mat == 0) {
 #pragma unroll
-      for (int c = 0; c < NC; ++c) gbuf[wave][c][lane] = acc[c];
+      for (int sr = 0; sr < NR; ++sr)
+#pragma unroll
+        for (int c = 0; c < NC; ++c) gbuf[wave][sr][c][lane] = acc[sr][c];
     }
     __syncthreads();
     if (mat == 0) return;
   }
-  if (!active || rl >= nrows) return;
-  const int n = n0 + rl;
+  if (!active) return;
 #pragma unroll
-  for (int c = 0; c < NC; ++c) {
-    if (c >= nch) break;
-    f32x4 gv4 = acc[c];
-    if constexpr (GATEUP) gv4 = gbuf[wave & 1][c][lane];
+  for (int sr = 0; sr < NR; ++sr) {
+    if (16 * sr + rl >= nrows) continue;
+    const int n = n0 + 16 * sr + rl;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = c * 16 + 4 * g + r;
-      if (t >= M) continue;
-      const int64_t o = (int64_t)(r0 + t) * N + n;
-      if constexpr (GATEUP) {
-        const float gv = gv4[r], uv = acc[c][r];
-        if (out0) {  // pre-activations are kept only for a backward
-          out0[o] = f2bf(gv);
-          out1[o] = f2bf(uv);
+    for (int c = 0; c < NC; ++c) {
+      if (c >= nch) break;
+      f32x4 gv4 = acc[sr][c];
+      if constexpr (GATEUP) gv4 = gbuf[wave & 1][sr][c][lane];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = c * 16 + 4 * g + r;
+        if (t >= M) continue;
+        const int64_t o = (int64_t)(r0 + t) * N + n;
+        if constexpr (GATEUP) {
+          const float gv = gv4[r], uv = acc[sr][c][r];
+          if (out0) {  // pre-activations are kept only for a backward
+            out0[o] = f2bf(gv);
+            out1[o] = f2bf(uv);
+          }
+          out2[o] = f2bf(silu_f(gv) * uv);
+        } else {
+          out0[o] = f2bf(acc[sr][c][r]);
         }
-        out2[o] = f2bf(silu_f(gv) * uv);
-      } else {
-        out0[o] = f2bf(acc[c][r]);
       }
     }
   }

@@ -369,10 +369,8 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
     int* bb = (int*)(ws + W.block_base);
     hipLaunchKernelGGL(k_hist, dim3(nb), dim3(256), sizeof(int) * E, s, idx, T, k, E, bh);
     hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bh, nb, E, bb, counts, offsets, tprefix);
-    int nbits = 0;
-    while ((1 << nbits) <= E) ++nbits;
-    hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), sizeof(int) * 8 * E, s, idx, T, k, E,
-                       nbits, bb, perm, inv);
+    hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), sizeof(int) * 16 * E, s, idx, T, k, E,
+                       bb, perm, inv);
     LAUNCH_CHECK();
   }
   return MOE_OK;
@@ -449,21 +447,21 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   const int H = p->cfg.hidden, S = p->cfg.shared_intermediate;
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   if (skinny && T <= 16) {
-    hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
+    hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, 32 * kSkinnyNR)), dim3(256), 0, ss,
                        (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
                        nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
                        (bf16_t*)sA);
     if (sY)
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, 64 * kSkinnyNR)), dim3(256), 0, ss,
                          (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else if (skinny) {
-    hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32)), dim3(256), 0, ss,
+    hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, 32 * kSkinnyNR)), dim3(256), 0, ss,
                        (const bf16_t*)x, nullptr, T, nullptr, (const bf16_t*)w->shared_gate,
                        nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
                        (bf16_t*)sA);
     if (sY)
-      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64)), dim3(256), 0, ss,
+      hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, 64 * kSkinnyNR)), dim3(256), 0, ss,
                          (const bf16_t*)sA, nullptr, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else {
@@ -505,12 +503,12 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   {
     StageTimer tm(p, s, stage(MOE_STAGE_GATEUP_FWD));
     if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, 32 * kSkinnyNR)), dim3(256), 0, s,
                          (const bf16_t*)st.xp, st.offsets, 0, (const bf16_t* const*)tg, nullptr,
                          (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G, (bf16_t*)st.U,
                          (bf16_t*)st.A);
       if (T > 16)
-        hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(E * ceil_div(I, 32)), dim3(256), 0, s,
+        hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(E * ceil_div(I, 32 * kSkinnyNR)), dim3(256), 0, s,
                            (const bf16_t*)st.xp, st.offsets, 0, (const bf16_t* const*)tg,
                            nullptr, (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G,
                            (bf16_t*)st.U, (bf16_t*)st.A);
@@ -524,11 +522,11 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   {
     StageTimer tm(p, s, stage(MOE_STAGE_DOWN_FWD));
     if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, 64)), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, 64 * kSkinnyNR)), dim3(256), 0, s,
                          (const bf16_t*)st.A, st.offsets, 0, (const bf16_t* const*)td, nullptr,
                          nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
       if (T > 16)
-        hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(E * ceil_div(H, 64)), dim3(256), 0,
+        hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(E * ceil_div(H, 64 * kSkinnyNR)), dim3(256), 0,
                            s, (const bf16_t*)st.A, st.offsets, 0, (const bf16_t* const*)td,
                            nullptr, nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
     } else {
@@ -598,7 +596,9 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
   {
     StageTimer tm(p, s, MOE_STAGE_COMBINE_FWD);
-    hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, st.Y, st.inv,
+    const int nsl = ceil_div(H / (16 / (int)sizeof(D)), kCombineSlice);
+    hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div((int64_t)T * nsl, 4)), dim3(256), 0, s,
+                       st.Y, st.inv,
                        st.w, sY, c.shared_expert_scale, T, k, H, resid, out);
     LAUNCH_CHECK();
   }
