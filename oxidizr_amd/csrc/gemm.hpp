@@ -244,7 +244,8 @@ struct DmaStager {
     k_valid[1] = d.k_valid;
   }
   MOE_DEV void issue(T* tile, int k0, int seg) const {
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: the LDS destination (M0) is then scalar arithmetic
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const uint32_t soff = (uint32_t)k0 * sizeof(T);
     const bool kin = k0 + kcol < k_valid[seg];
 #pragma unroll
@@ -282,7 +283,8 @@ struct DmaStagerT {
   }
   MOE_DEV void init_second(const OpDesc<T>& d) { rs[1] = rsrc_of(d); }
   MOE_DEV void issue(T* tile, int k0, int seg) const {
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: the LDS destination (M0) is then scalar arithmetic
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
