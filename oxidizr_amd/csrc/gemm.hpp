@@ -414,8 +414,12 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
 // main loop with NA A operands and NB B operands.
 template <class C, int NA, int NB>
 constexpr int stage_elems() { return (NA * C::BM + NB * C::BN) * C::LDK; }
+// 16-bit operands always take the direct-to-LDS loop, whose tiles are
+// unpadded; fp32 keeps the padded pitch of the register-staged loop.
 template <class C, int NA, int NB>
-constexpr int smem_elems() { return 2 * stage_elems<C, NA, NB>(); }
+constexpr int smem_elems() {
+  return C::V == 8 ? 2 * (NA * C::BM + NB * C::BN) * C::BK : 2 * stage_elems<C, NA, NB>();
+}
 
 // acc[a * NB + b][tn][tm] += B_b-tile x A_a-tile over k in [0, K).
 // Two LDS stages: while the waves multiply out of stage kt & 1, the k-tile

@@ -145,7 +145,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
                                                        float* __restrict__ logits, int Tn, int H,
                                                        int E) {
   using C = typename Tilings<T>::Router;
-  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   RowGroups g{nullptr, nullptr, 1, Tn};
   int grp, row0, mv, n0;
   if (!resolve_rows(g, E, C::BM, C::BN, grp, row0, mv, n0)) return;
@@ -478,14 +478,15 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // only when G is not null (a forward that keeps state for a backward).
 // GROUPED: expert row groups (offsets set); otherwise one dense group (a
 // separate instantiation, so profiles tell the two launches apart).
-template <typename T, bool GROUPED>
+// C: the tiling (Tilings<T>::GateUp, or 128-row tiles for experts with few
+// rows, whose last row tile would otherwise be mostly padding).
+template <typename T, bool GROUPED, class C = typename Tilings<T>::GateUp>
 __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
                                                     const T* const* wg_tab, const T* wg_one,
                                                     const T* const* wu_tab, const T* wu_one,
                                                     int H, int N, T* __restrict__ G,
                                                     T* __restrict__ U, T* __restrict__ A) {
-  using C = typename Tilings<T>::GateUp;
-  __shared__ __align__(16) T smem[smem_elems<C, 1, 2>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 2, 2>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);
@@ -511,12 +512,11 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
 }
 
 // Y = A Wd^T per row group (K = I) or for the dense shared expert.
-template <typename T, bool GROUPED>
+template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
                                                   const T* const* wd_tab, const T* wd_one, int I,
                                                   int H, T* __restrict__ Y) {
-  using C = typename Tilings<T>::Big;
-  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);
@@ -637,14 +637,13 @@ __global__ __launch_bounds__(256) void k_combine_bwd(const T* __restrict__ dout,
 // ------------------------------------------------------------------ expert GEMMs (backward)
 // dA = alpha * dY Wd (NN, K = H), then the SwiGLU backward in the epilogue:
 // dG = dA * U * silu'(G), dU = dA * silu(G).
-template <typename T, bool GROUPED>
+template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, RowGroups groups,
                                                     const T* const* wd_tab, const T* wd_one,
                                                     int H, int N, float alpha,
                                                     const T* __restrict__ G,
                                                     const T* __restrict__ U,
                                                     T* __restrict__ dG, T* __restrict__ dU) {
-  using C = typename Tilings<T>::Big;
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
@@ -692,14 +691,13 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
 }
 
 // dX = dG Wg + dU Wu (NN, K = I twice) per row group.
-template <typename T, bool GROUPED>
+template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
                                                       const T* __restrict__ dU, RowGroups groups,
                                                       const T* const* wg_tab, const T* wg_one,
                                                       const T* const* wu_tab, const T* wu_one,
                                                       int I, int H, T* __restrict__ dX) {
-  using C = typename Tilings<T>::Big;
-  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);  // [I, H]: element (n=h, k=i) at wg + i*H + h
@@ -731,7 +729,7 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
                                                T* const* out1_tab, T* out1_one,
                                                float* __restrict__ partial) {
   using C = typename std::conditional<NA == 2, typename Tilings<T>::WgradPair, typename Tilings<T>::Big>::type;
-  __shared__ __align__(16) T smem[smem_elems<C, NA, 1>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, NA, 1, NA>()];
   int grp, split, krow0, K, m0, n0;
   if (!resolve_k(groups, M, N, C::BM, C::BN, grp, split, krow0, K, m0, n0)) return;
   OpDesc<T> a[NA];
@@ -858,7 +856,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
                                                       const T* __restrict__ dxs,
                                                       T* __restrict__ dx) {
   using C = typename Tilings<T>::Router;
-  __shared__ __align__(16) T smem[smem_elems<C, 1, 1>()];
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   RowGroups g{nullptr, nullptr, 1, Tn};
   int grp, row0, mv, n0;
   if (!resolve_rows(g, H, C::BM, C::BN, grp, row0, mv, n0)) return;
