@@ -104,10 +104,16 @@ MOE_DEV float wave_max(float v) {
   return v;
 }
 
-// Map a linear workgroup id so that the blocks one XCD receives (ids are
-// dealt round-robin over the 8 XCDs) form one contiguous range of logical
-// tiles: neighbouring tiles then share that XCD's L2.
-MOE_DEV int xcd_remap(int id, int n) {
-  const int x = id & 7, q = n >> 3, r = n & 7;
-  return x * q + (x < r ? x : r) + (id >> 3);
+// Map workgroup b to a logical tile id in [0, n) so that the blocks one XCD
+// receives (blocks are dealt round-robin over the 8 XCDs) form one contiguous
+// range of logical tiles, and neighbouring tiles share that XCD's L2.  The
+// ranges split the n tiles that exist (not the grid, which may be an upper
+// bound when n depends on the routing) evenly over the XCDs, so no XCD is
+// left idle by a grid larger than the work.  Returns false for blocks past
+// their XCD's range; needs a grid of at least n blocks.
+MOE_DEV bool xcd_slot(int b, int n, int& id) {
+  const int x = b & 7, j = b >> 3, q = n >> 3, r = n & 7;
+  if (j >= q + (x < r ? 1 : 0)) return false;
+  id = x * q + (x < r ? x : r) + j;
+  return true;
 }

@@ -53,7 +53,7 @@ struct RowGroups {
 MOE_DEV int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
 // Output-tile order.  Workgroup ids are first made contiguous per XCD
-// (xcd_remap); consecutive ids then walk GM row-tiles down a tile column
+// (xcd_slot); consecutive ids then walk GM row-tiles down a tile column
 // before moving one column right, so the ~32 workgroups resident on one XCD
 // cover about GM A panels and 32 / GM B panels, which its L2 holds, instead of
 // one A panel and 32 B panels.  Returns false for ids past the nM x nN tiles.
@@ -72,9 +72,8 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
                           int& mv, int& n0) {
   const int nN = (N + BN - 1) / BN;
   const int nM = g.offsets == nullptr ? (g.M + BM - 1) / BM : g.tile_prefix[g.G];
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
-  int mt, nt;
-  if (!tile_order(id, nM, nN, mt, nt)) return false;
+  int id, mt, nt;
+  if (!xcd_slot(blockIdx.x, nM * nN, id) || !tile_order(id, nM, nN, mt, nt)) return false;
   n0 = nt * BN;
   if (g.offsets == nullptr) {
     grp = 0;
@@ -106,7 +105,8 @@ MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp,
                        int& krow0, int& K, int& m0, int& n0) {
   const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
   const int per = nM * nN;
-  const int id = xcd_remap(blockIdx.x, gridDim.x);
+  int id;
+  if (!xcd_slot(blockIdx.x, gridDim.x, id)) return false;
   const int gs = uni(id / per);   // group (grouped) or split chunk (dense)
   const int r = uni(id % per);
   m0 = uni(r / nN) * BM;
