@@ -104,11 +104,16 @@ struct KGroups {
 MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& split,
                        int& krow0, int& K, int& m0, int& n0) {
   const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
+  // Each group (or split chunk) owns 8 * ceil(per / 8) consecutive blocks and
+  // its per tiles are dealt over the 8 XCDs in contiguous ranges, so every XCD
+  // takes 1/8 of every group: the groups' token counts (the K of their tiles)
+  // differ widely, and whole groups per XCD would leave the XCD that holds the
+  // busiest expert running long after the others.
   const int per = nM * nN;
-  int id;
-  if (!xcd_slot(blockIdx.x, gridDim.x, id)) return false;
-  const int gs = uni(id / per);   // group (grouped) or split chunk (dense)
-  const int r = uni(id % per);
+  const int span = 8 * ((per + 7) >> 3);
+  const int gs = uni(blockIdx.x / span);   // group (grouped) or split chunk (dense)
+  int r;
+  if (!xcd_slot(blockIdx.x - gs * span, per, r)) return false;
   m0 = uni(r / nN) * BM;
   n0 = uni(r % nN) * BN;
   if (g.offsets) {

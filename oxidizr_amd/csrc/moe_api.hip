@@ -382,6 +382,12 @@ int tile_slot(int bm) {
   }
 }
 
+// Blocks of a K-grouped (weight-gradient) launch over `groups` groups or
+// split chunks of an M x N output: each takes 8 * ceil(tiles / 8) blocks.
+inline int kgrouped_grid(int groups, int M, int N, int BM, int BN) {
+  return groups * 8 * ceil_div(ceil_div(M, BM) * ceil_div(N, BN), 8);
+}
+
 // Weight gradient of a dense (all-token) GEMM: out_x[m, n] = alpha * sum_t
 // P_x[t, m] Q[t, n], split over tokens when that fills the GPU better.
 template <typename D, int NA>
@@ -392,8 +398,8 @@ void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, co
                                       typename Tilings<D>::Big>::type;
   const SplitPlan sp = plan_split<C>(M, N, T);
   const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk};
-  const int tiles = ceil_div(M, C::BM) * ceil_div(N, C::BN);
-  hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(tiles * sp.nsplit), dim3(256), 0, s, P0, P1, ldp, Q,
+  hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN)),
+                     dim3(256), 0, s, P0, P1, ldp, Q,
                      ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
   if (sp.nsplit > 1) {
     const int64_t MN = (int64_t)M * N;
@@ -762,7 +768,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_DOWN_WGRAD);
-    const int grid = E * ceil_div(H, CB::BM) * ceil_div(I, CB::BN);
+    const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
     hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
                        (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
@@ -778,7 +784,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_GATEUP_WGRAD);
-    const int grid = E * ceil_div(I, CW::BM) * ceil_div(H, CW::BN);
+    const int grid = kgrouped_grid(E, I, H, CW::BM, CW::BN);
     hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
                        (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
