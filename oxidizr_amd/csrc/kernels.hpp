@@ -1096,9 +1096,35 @@ MOE_DEV const T* uni_ptr(const T* p) {
   return (const T*)(((uint64_t)hi << 32) | lo);
 }
 
+// The expert holding the j-th (from 0) group of more than 16 rows, or -1:
+// each wave counts the wide groups 64 at a time with a ballot.  Uniform.
+MOE_DEV int nth_wide_group(const int* offsets, int G, int j) {
+  const int lane = threadIdx.x & 63;
+  int seen = 0;
+  for (int base = 0; base < G; base += 64) {
+    const int e = base + lane;
+    const bool wide = e < G && offsets[e + 1] - offsets[e] > 16;
+    uint64_t m = __ballot(wide);
+    const int n = __popcll(m);
+    if (j < seen + n) {
+      for (int i = seen; i < j; ++i) m &= m - 1;  // drop the lower wide groups
+      return uni(base + __ffsll((unsigned long long)m) - 1);
+    }
+    seen += n;
+  }
+  return -1;
+}
+// Routed launches of the WIDE kernel need blocks for at most this many groups.
+inline int max_wide_groups(int64_t rows, int G) {
+  const int64_t w = rows / 17;
+  return (int)(w < G ? w : G);
+}
+
 // WIDE = false handles the experts with at most 16 tokens (one chunk of token
 // rows), WIDE = true those with 17..64; both are launched and each skips the
-// other's experts.  A workgroup owns 64 consecutive weight rows (16 per wave)
+// other's experts.  The WIDE launch of a grouped problem is sized for the
+// most groups that can hold 17 rows (rows / 17) and its block j / nNb takes
+// the (j / nNb)-th such group.  A workgroup owns 64 consecutive weight rows (16 per wave)
 // of one expert.  GATEUP: each wave streams its 16 gate rows over all of K,
 // then the same 16 up rows, and applies SwiGLU in registers (a lane holds the
 // gate and up values of the same outputs), so at any time a workgroup reads
@@ -1108,7 +1134,8 @@ MOE_DEV const T* uni_ptr(const T* p) {
 // its MFMAs, so they overlap each other instead of one L2 latency per MFMA.
 template <bool GATEUP, bool WIDE>
 __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X,
-                                                    const int* __restrict__ offsets, int Mdense,
+                                                    const int* __restrict__ offsets, int ngroups,
+                                                    int Mdense,
                                                     const bf16_t* const* w0_tab, const bf16_t* w0_one,
                                                     const bf16_t* const* w1_tab, const bf16_t* w1_one,
                                                     int K, int N, bf16_t* __restrict__ out0,
@@ -1118,7 +1145,9 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
   constexpr int NC = WIDE ? 4 : 1;
   constexpr int NM = GATEUP ? 2 : 1;  // weight matrices streamed in turn
   const int nNb = (N + ROWS_PER_WG - 1) / ROWS_PER_WG;
-  const int e = uni(blockIdx.x / nNb), nb = uni(blockIdx.x % nNb);
+  const int slot = uni(blockIdx.x / nNb), nb = uni(blockIdx.x % nNb);
+  const int e = WIDE && offsets ? nth_wide_group(offsets, ngroups, slot) : slot;
+  if (e < 0) return;
   const int r0 = offsets ? offsets[e] : 0;
   const int M = offsets ? offsets[e + 1] - r0 : Mdense;
   if (M <= 0 || (WIDE ? M <= 16 : M > 16)) return;
@@ -1225,6 +1254,7 @@ __global__ __launch_bounds__(256) void k_router_small(const bf16_t* __restrict__
         const bool kin = kc * 256 + 32 * q + 8 * g < H;
         xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
       }
+      __builtin_amdgcn_sched_barrier(0);  // all token loads in flight before the MFMAs
 #pragma unroll
       for (int q = 0; q < 8; ++q) mfma16(acc[c], xa[q], wa[q]);
     }

@@ -159,6 +159,7 @@ SKINNY_CASES = [
     dict(T=48, H=256, E=32, k=4, I=96, S=64),
     dict(T=64, H=136, E=4, k=4, I=40, S=0),        # every expert gets all 64 tokens
     dict(T=7, H=72, E=6, k=2, I=24, S=16),
+    dict(T=64, H=200, E=8, k=2, I=72, S=24),       # ~16 rows per expert: both kernels
 ]
 
 
