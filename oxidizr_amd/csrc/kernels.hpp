@@ -1215,63 +1215,52 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
   }
 }
 
-// Router logits for T <= kSkinnyMaxTokens (bf16): a workgroup owns 16
-// experts, its four waves take every fourth 256-wide k-chunk of the hidden
-// dimension (same lane layout as k_skinny_fwd), and the partial sums are added
-// through LDS in wave order.
-__global__ __launch_bounds__(256) void k_router_small(const bf16_t* __restrict__ x,
+// Router logits for T <= kSkinnyMaxTokens (bf16): workgroup (x, y) owns 16
+// experts and 16 tokens; its kRouterWaves waves take every kRouterWaves-th
+// 256-wide k-chunk of the hidden dimension (same lane layout as k_skinny_fwd)
+// and the partial sums are added through LDS in wave order.  With few experts
+// the launch is small, so the work is cut finely (H = 4096: one chunk per
+// wave, 16 token rows per workgroup): one CU cannot pull the whole token
+// matrix quickly.
+constexpr int kRouterWaves = 16;
+__global__ __launch_bounds__(64 * kRouterWaves) void k_router_small(const bf16_t* __restrict__ x,
                                                       const bf16_t* __restrict__ wr,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ logits, int Tn, int H,
                                                       int E) {
-  __shared__ f32x4 red[4][4][64];
-  const int e0 = blockIdx.x * 16;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  __shared__ f32x4 red[kRouterWaves][64];
+  const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+  const int wave = uni(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int g = lane >> 4, rl = lane & 15;
-  const int nrows = min(16, E - e0);
+  const int nrows = min(16, E - e0), ntok = min(16, Tn - t0);
   const rsrc_t rw = make_rsrc(wr + (int64_t)e0 * H, (uint32_t)((int64_t)nrows * H * 2));
-  const rsrc_t rx = make_rsrc(x, (uint32_t)((int64_t)Tn * H * 2));
-  const int nch = (Tn + 15) / 16;
+  const rsrc_t rx = make_rsrc(x + (int64_t)t0 * H, (uint32_t)((int64_t)ntok * H * 2));
   const uint32_t vw = (uint32_t)((rl * H + 8 * g) * 2);
-  f32x4 acc[4];
-#pragma unroll
-  for (int c = 0; c < 4; ++c) acc[c] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int kc = wave; kc * 256 < H; kc += 4) {
+  f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kc = wave; kc * 256 < H; kc += kRouterWaves) {
     const uint32_t soff = (uint32_t)kc * 512;
-    u32x4 wa[8];
+    u32x4 wa[8], xa[8];
 #pragma unroll
     for (int q = 0; q < 8; ++q) {
       const bool kin = kc * 256 + 32 * q + 8 * g < H;
       wa[q] = buf_ld16(rw, kin ? vw + 64 * q : kOobOffset, soff);
+      xa[q] = buf_ld16(rx, kin ? vw + 64 * q : kOobOffset, soff);
     }
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if (c >= nch) break;
-      const uint32_t vx = (uint32_t)(((c * 16 + rl) * H + 8 * g) * 2);
-      u32x4 xa[8];
-#pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const bool kin = kc * 256 + 32 * q + 8 * g < H;
-        xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
-      }
-      __builtin_amdgcn_sched_barrier(0);  // all token loads in flight before the MFMAs
-#pragma unroll
-      for (int q = 0; q < 8; ++q) mfma16(acc[c], xa[q], wa[q]);
-    }
+    for (int q = 0; q < 8; ++q) mfma16(acc, xa[q], wa[q]);
   }
-#pragma unroll
-  for (int c = 0; c < 4; ++c) red[wave][c][lane] = acc[c];
+  red[wave][lane] = acc;
   __syncthreads();
   if (wave != 0 || rl >= nrows) return;
   const int e = e0 + rl;
   const float b = bias ? bias[e] : 0.0f;
-  for (int c = 0; c < nch; ++c) {
-    const f32x4 v = ((red[0][c][lane] + red[1][c][lane]) + red[2][c][lane]) + red[3][c][lane];
+  f32x4 v = red[0][lane];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = c * 16 + 4 * g + r;
-      if (t < Tn) logits[(int64_t)t * E + e] = v[r] + b;
-    }
+  for (int w = 1; w < kRouterWaves; ++w) v += red[w][lane];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int t = 4 * g + r;  // lane holds D[token t0 + 4 g + r][expert e0 + rl]
+    if (t < ntok) logits[(int64_t)(t0 + t) * E + e] = v[r] + b;
   }
 }
 

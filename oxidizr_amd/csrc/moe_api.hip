@@ -617,7 +617,8 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   {
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
     if (std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens) {
-      hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16)), dim3(256), 0, s, (const bf16_t*)x,
+      hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16), ceil_div(T, 16)),
+                         dim3(64 * kRouterWaves), 0, s, (const bf16_t*)x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
                          st.logits, T, H, E);
     } else {
