@@ -170,16 +170,13 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
 }
 
 // ------------------------------------------------------------------ routing
-// One wave per token: softmax(logits / tau), log-sum-exp, top-k on the raw
-// logits (NaN selects as -inf; equal values -> lower expert index first).
+// One wave routes token t: softmax(logits / tau), log-sum-exp, top-k on the
+// raw logits (NaN selects as -inf; equal values -> lower expert index first).
 template <int EPL>
-__global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int Tn, int E,
-                                               int k, float tau, int norm,
-                                               float* __restrict__ probs, float* __restrict__ lse,
-                                               int* __restrict__ idx, float* __restrict__ w) {
+MOE_DEV void route_one(const float* __restrict__ logits, int t, int E, int k, float tau,
+                       int norm, float* __restrict__ probs, float* __restrict__ lse,
+                       int* __restrict__ idx, float* __restrict__ w) {
   const int lane = threadIdx.x & 63;
-  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (t >= Tn) return;
   const float* row = logits + (int64_t)t * E;
   float v[EPL], ex[EPL];
   float mx = -INFINITY;
@@ -250,6 +247,17 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
       w[(int64_t)t * k + j] = norm ? wsel[j] / wsum : wsel[j];
     }
   }
+}
+
+// One wave per token.
+template <int EPL>
+__global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits, int Tn, int E,
+                                               int k, float tau, int norm,
+                                               float* __restrict__ probs, float* __restrict__ lse,
+                                               int* __restrict__ idx, float* __restrict__ w) {
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
+  route_one<EPL>(logits, t, E, k, tau, norm, probs, lse, idx, w);
 }
 
 // ------------------------------------------------------------------ column sums
@@ -351,6 +359,30 @@ MOE_DEV int wave_incl_scan(int v) {
   return v;
 }
 
+// With cnt[e] (LDS, e < E <= 1024) in place, a block of 1024 threads writes
+// the exclusive offsets (also to offs, LDS) and the tile prefix of every
+// height in kTileBM, one expert per thread.  Integer arithmetic only.
+MOE_DEV void scan_counts(const int* cnt, int E, int* __restrict__ offsets,
+                         int* __restrict__ tile_prefix, int* offs, int* wsum) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  for (int j = 0; j <= kNumTileBM; ++j) {
+    const int bm = j == 0 ? 1 : kTileBM[j - 1];
+    const int v = tid < E ? (cnt[tid] + bm - 1) / bm : 0;
+    const int incl = wave_incl_scan(v);
+    if (lane == 63) wsum[wave] = incl;
+    __syncthreads();
+    int base = 0;
+    for (int w = 0; w < wave; ++w) base += wsum[w];
+    int* dst = j == 0 ? offsets : tile_prefix + (j - 1) * (E + 1);
+    if (tid < E) {
+      dst[tid] = base + incl - v;
+      if (j == 0) offs[tid] = base + incl - v;
+    }
+    if (tid == 1023) dst[E] = base + incl;
+    __syncthreads();
+  }
+}
+
 // One block of 1024 threads (E <= 1024).  Thread (g, e) = (tid / E, tid % E)
 // owns expert e's histogram entries of a contiguous chunk of blocks: the
 // chunk sums and their exclusive prefix over g give the expert counts and the
@@ -364,7 +396,7 @@ __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_his
                                                int* __restrict__ tile_prefix) {
   __shared__ int cnt[1024], offs[1024], part[1024];
   __shared__ int wsum[16];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x;
   const int G = 1024 / E;            // threads per expert
   const int e = tid % E, g = tid / E;
   const bool act = g < G;
@@ -385,22 +417,7 @@ __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_his
     counts[tid] = run;
   }
   __syncthreads();
-  for (int j = 0; j <= kNumTileBM; ++j) {
-    const int bm = j == 0 ? 1 : kTileBM[j - 1];
-    const int v = tid < E ? (cnt[tid] + bm - 1) / bm : 0;
-    const int incl = wave_incl_scan(v);
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
-    int base = 0;
-    for (int w = 0; w < wave; ++w) base += wsum[w];
-    int* dst = j == 0 ? offsets : tile_prefix + (j - 1) * (E + 1);
-    if (tid < E) {
-      dst[tid] = base + incl - v;
-      if (j == 0) offs[tid] = base + incl - v;
-    }
-    if (tid == 1023) dst[E] = base + incl;
-    __syncthreads();
-  }
+  scan_counts(cnt, E, offsets, tile_prefix, offs, wsum);
   if (act) {
     int run = offs[e] + part[tid];
     for (int b = b0; b < b1; ++b) {
@@ -457,6 +474,75 @@ __global__ __launch_bounds__(256) void k_scatter(const int* __restrict__ idx, in
     const int pos = block_base[(int64_t)blockIdx.x * E + e] + wbase[wave * E + e] + rank;
     perm[pos] = t * k + j;
     inv_perm[(int64_t)t * k + j] = pos;
+  }
+}
+
+// Dispatch of a small batch (T <= kRouteSmallTokens, after k_route) in one
+// workgroup of 1024 threads, with the bits of the multi-kernel path: P is
+// summed in k_colsum_partial's order (four running sums over t mod 4, added
+// in order, one lane each) and scaled as k_colsum_final does; counts,
+// offsets and tile prefixes come from scan_counts; the rank of assignment
+// (t, j) within its expert is the number of earlier tokens that chose the
+// expert, read from a 64-bit token mask per expert (built with LDS atomic
+// ORs, which do not depend on order).
+constexpr int kRouteSmallTokens = 64;
+__global__ __launch_bounds__(1024) void k_dispatch_small(const int* __restrict__ idx,
+                                                         const float* __restrict__ probs, int Tn,
+                                                         int E, int k, float scale,
+                                                         float* __restrict__ P,
+                                                         int* __restrict__ counts,
+                                                         int* __restrict__ offsets,
+                                                         int* __restrict__ tile_prefix,
+                                                         int* __restrict__ perm,
+                                                         int* __restrict__ inv_perm) {
+  __shared__ int sidx[kRouteSmallTokens * 16];
+  __shared__ unsigned tmask[1024][2];
+  __shared__ int cnt[1024], offs[1024], wsum[16];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) tmask[e][0] = tmask[e][1] = 0u;
+  for (int i = tid; i < Tn * k; i += 1024) sidx[i] = idx[i];
+  // P: lanes 4e + q hold the running sum over tokens t = q mod 4
+  for (int e0 = 0; e0 < E; e0 += 256) {
+    const int e = e0 + (tid >> 2), q = tid & 3;
+    float r = 0.0f;
+    if (e < E) {
+      float v[kRouteSmallTokens / 4];
+#pragma unroll
+      for (int i = 0; i < kRouteSmallTokens / 4; ++i) {
+        const int t = q + 4 * i;
+        v[i] = t < Tn ? probs[(int64_t)t * E + e] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < kRouteSmallTokens / 4; ++i)
+        if (q + 4 * i < Tn) r += v[i];
+    }
+    const int base = threadIdx.x & 60;  // lanes 4e .. 4e + 3 of this wave
+    const float r0 = __shfl(r, base, 64), r1 = __shfl(r, base + 1, 64);
+    const float r2 = __shfl(r, base + 2, 64), r3 = __shfl(r, base + 3, 64);
+    // k_colsum_final adds this single partial to three zeros: the same value
+    if (e < E && q == 0) P[e] = (((r0 + r1) + r2) + r3) * scale;
+  }
+  __syncthreads();
+  for (int i = tid; i < Tn * k; i += 1024) {
+    const int t = i / k;
+    atomicOr(&tmask[sidx[i]][t >> 5], 1u << (t & 31));
+  }
+  __syncthreads();
+  if (tid < E) {
+    const int c = __popc(tmask[tid][0]) + __popc(tmask[tid][1]);
+    cnt[tid] = c;
+    counts[tid] = c;
+  }
+  __syncthreads();
+  scan_counts(cnt, E, offsets, tile_prefix, offs, wsum);
+  for (int i = tid; i < Tn * k; i += 1024) {
+    const int t = i / k, e = sidx[i];
+    const unsigned lo = tmask[e][0], hi = tmask[e][1];
+    const int rank = t < 32 ? __popc(lo & ((1u << t) - 1u))
+                            : __popc(lo) + __popc(hi & ((1u << (t - 32)) - 1u));
+    const int pos = offs[e] + rank;
+    perm[pos] = i;
+    inv_perm[i] = pos;
   }
 }
 
@@ -1134,6 +1220,8 @@ inline int max_wide_groups(int64_t rows, int G) {
 // its MFMAs, so they overlap each other instead of one L2 latency per MFMA.
 template <bool GATEUP, bool WIDE>
 __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X,
+                                                    const int* __restrict__ xrow, int kdiv,
+                                                    int xrows,
                                                     const int* __restrict__ offsets, int ngroups,
                                                     int Mdense,
                                                     const bf16_t* const* w0_tab, const bf16_t* w0_one,
@@ -1156,9 +1244,19 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
   const int nrows = uni(min(16, N - n0));
   if (nrows <= 0) return;  // wave-uniform; no barrier follows
   const int g = lane >> 4, rl = lane & 15;
-  const rsrc_t rx = make_rsrc(uni_ptr(X + (int64_t)r0 * K), (uint32_t)uni(M * K * 2));
+  // token row i of the group: row r0 + i of X, or (xrow != null) row
+  // xrow[r0 + i] / kdiv of X (the assignment's token: no gathered copy)
+  const rsrc_t rx = xrow ? make_rsrc(uni_ptr(X), (uint32_t)uni(xrows * K * 2))
+                         : make_rsrc(uni_ptr(X + (int64_t)r0 * K), (uint32_t)uni(M * K * 2));
   const int nch = (M + 15) / 16;
   const uint32_t vw = (uint32_t)((rl * K + 8 * g) * 2);
+  uint32_t vxc[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int i = c * 16 + rl;
+    const int row = i >= M ? -1 : xrow ? xrow[r0 + i] / kdiv : i;
+    vxc[c] = row < 0 ? kOobOffset : (uint32_t)((row * K + 8 * g) * 2);
+  }
   f32x4 acc[NM][NC];
 #pragma unroll
   for (int m = 0; m < NM; ++m) {
@@ -1177,12 +1275,11 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         if (c >= nch) break;
-        const uint32_t vx = (uint32_t)(((c * 16 + rl) * K + 8 * g) * 2);
         u32x4 xa[8];
 #pragma unroll
         for (int q = 0; q < 8; ++q) {
           const bool kin = kc * 256 + 32 * q + 8 * g < K;
-          xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
+          xa[q] = buf_ld16(rx, kin ? vxc[c] + 64 * q : kOobOffset, soff);
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll

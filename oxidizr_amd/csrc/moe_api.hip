@@ -354,6 +354,12 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
       default: launch_route<16>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
     }
     LAUNCH_CHECK();
+    if (T <= kRouteSmallTokens) {  // P and the whole dispatch in one workgroup
+      hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, s, idx, probs, T, E, k,
+                         1.0f / (float)T, P, counts, offsets, tprefix, perm, inv);
+      LAUNCH_CHECK();
+      return MOE_OK;
+    }
     const int nrb = ceil_div(T, 64);
     float* part = (float*)(ws + W.colpart);
     hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, probs, T,
@@ -454,21 +460,21 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   if (skinny && T <= 16) {
     hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, kSkinnyRows)), dim3(256), 0, ss,
-                       (const bf16_t*)x, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_gate,
+                       (const bf16_t*)x, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_gate,
                        nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
                        (bf16_t*)sA);
     if (sY)
       hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, kSkinnyRows)), dim3(256), 0, ss,
-                         (const bf16_t*)sA, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
+                         (const bf16_t*)sA, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else if (skinny) {
     hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(ceil_div(S, kSkinnyRows)), dim3(256), 0, ss,
-                       (const bf16_t*)x, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_gate,
+                       (const bf16_t*)x, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_gate,
                        nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
                        (bf16_t*)sA);
     if (sY)
       hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(ceil_div(H, kSkinnyRows)), dim3(256), 0, ss,
-                         (const bf16_t*)sA, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
+                         (const bf16_t*)sA, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else {
     const RowGroups dense{nullptr, nullptr, 1, T};
@@ -518,31 +524,35 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   const moe_config& c = p->cfg;
   const int H = c.hidden, E = c.num_experts, k = c.experts_per_tok, I = c.intermediate;
   const int64_t TK = (int64_t)T * k;
-  const int* tprefix = st.tprefix + tile_slot(CB::BM) * (E + 1);
   auto stage = [&](int id) { return timed ? id : MOE_STAGE_RECOMPUTE; };
-  {
+  // few tokens: no expert holds more than T rows, stream the weights instead
+  const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
+  // X_perm is read by the tiled GEMMs and, when the gate / up pre-activations
+  // are kept (a backward follows and reads saved state), by the weight
+  // gradient; otherwise the small-token kernel reads each assignment's token
+  // row of x directly.
+  const bool gather = !skinny || st.G != nullptr;
+  if (gather) {
     StageTimer tm(p, s, stage(MOE_STAGE_GATHER));
     hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(TK, 4)), dim3(256), 0, s, x, st.perm, T, k, H,
                        st.xp);
     LAUNCH_CHECK();
   }
+  const bf16_t* xsrc = (const bf16_t*)(gather ? st.xp : x);
+  const int* xrow = gather ? nullptr : st.perm;
   const D* const* tg = (const D* const*)p->d_tab;
   const D* const* tu = (const D* const*)(p->d_tab + E);
   const D* const* td = (const D* const*)(p->d_tab + 2 * E);
-  const RowGroups rg{st.offsets, tprefix, E, (int)TK};
-  const int mtiles_max = ceil_div(TK, CB::BM) + E;
-  // few tokens: no expert holds more than T rows, stream the weights instead
-  const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   {
     StageTimer tm(p, s, stage(MOE_STAGE_GATEUP_FWD));
     if (skinny) {
       hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, kSkinnyRows)), dim3(256), 0, s,
-                         (const bf16_t*)st.xp, st.offsets, E, 0, (const bf16_t* const*)tg, nullptr,
+                         xsrc, xrow, k, T, st.offsets, E, 0, (const bf16_t* const*)tg, nullptr,
                          (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G, (bf16_t*)st.U,
                          (bf16_t*)st.A);
       if (T > 16)
         hipLaunchKernelGGL((k_skinny_fwd<true, true>), dim3(max_wide_groups(TK, E) * ceil_div(I, kSkinnyRows)), dim3(256), 0, s,
-                           (const bf16_t*)st.xp, st.offsets, E, 0, (const bf16_t* const*)tg,
+                           xsrc, xrow, k, T, st.offsets, E, 0, (const bf16_t* const*)tg,
                            nullptr, (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G,
                            (bf16_t*)st.U, (bf16_t*)st.A);
     } else {
@@ -558,11 +568,11 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
     StageTimer tm(p, s, stage(MOE_STAGE_DOWN_FWD));
     if (skinny) {
       hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, kSkinnyRows)), dim3(256), 0, s,
-                         (const bf16_t*)st.A, st.offsets, E, 0, (const bf16_t* const*)td, nullptr,
+                         (const bf16_t*)st.A, nullptr, 1, 0, st.offsets, E, 0, (const bf16_t* const*)td, nullptr,
                          nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
       if (T > 16)
         hipLaunchKernelGGL((k_skinny_fwd<false, true>), dim3(max_wide_groups(TK, E) * ceil_div(H, kSkinnyRows)), dim3(256), 0,
-                           s, (const bf16_t*)st.A, st.offsets, E, 0, (const bf16_t* const*)td,
+                           s, (const bf16_t*)st.A, nullptr, 1, 0, st.offsets, E, 0, (const bf16_t* const*)td,
                            nullptr, nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
     } else {
       with_row_tiling<CB, D, false>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
@@ -684,7 +694,6 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   const State<D> st(rb, LR, ab, LA);
   const int* counts = st.counts;
   const int* offsets = st.offsets;
-  const int* tprefix = st.tprefix + tile_slot(CB::BM) * (E + 1);
   const int* inv = st.inv;
   const int* idx = st.idx;
   const float* topw = st.w;
@@ -709,10 +718,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdg = (D* const*)(p->d_tab + 3 * E);
   D* const* tdu = (D* const*)(p->d_tab + 4 * E);
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
-  const RowGroups rg{offsets, tprefix, E, (int)TK};
   const KGroups kg{offsets, E, 0, 1, 0};
   float* partial = (float*)(ws + W.splitk_router);
-  const int mtiles_max = ceil_div(TK, CB::BM) + E;
   // Shared expert backward first, on the plan's second stream: it needs only
   // d_out, x and its own saved activations; dx waits for it below.
   D* dxs = nullptr;
@@ -927,12 +934,13 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
 
 moe_status moe_plan_destroy(moe_plan* p) {
   if (!p) return MOE_OK;
+  // teardown: nothing to report if a release fails
   for (auto& q : p->pending) {
-    hipEventSynchronize(q.b);
-    hipEventDestroy(q.a);
-    hipEventDestroy(q.b);
+    (void)hipEventSynchronize(q.b);
+    (void)hipEventDestroy(q.a);
+    (void)hipEventDestroy(q.b);
   }
-  for (auto e : p->free_events) hipEventDestroy(e);
+  for (auto e : p->free_events) (void)hipEventDestroy(e);
   if (p->aux) (void)hipStreamSynchronize(p->aux);
   if (p->fork) (void)hipEventDestroy(p->fork);
   if (p->join) (void)hipEventDestroy(p->join);
