@@ -150,8 +150,14 @@ struct moe_plan {
   // within each call, and fills the routed GEMMs' partial rounds of work.
   hipStream_t aux = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  // The backward's routed weight gradients and the router backward need only
+  // dY / dG / dU and the routing state: they run on a third stream, beside
+  // the input-gradient GEMMs of the call's stream.
+  hipStream_t wgs = nullptr;
+  hipEvent_t wfork = nullptr, wmid = nullptr, wjoin = nullptr;
   bool overlap = true;
   hipStream_t shared_stream(hipStream_t s) const { return overlap && aux ? aux : s; }
+  hipStream_t wgrad_stream(hipStream_t s) const { return overlap && wgs ? wgs : s; }
 
   int E() const { return cfg.num_experts; }
   int es() const { return elt_size(cfg.dtype); }
@@ -765,6 +771,44 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                        topw, T, k, H, dw, dY);
     LAUNCH_CHECK();
   }
+  // From here the router backward and the routed weight gradients run on the
+  // weight-gradient stream ws2 (they read dw, dY, A, X_perm and, after the
+  // down projection's input gradient, dG / dU), the input gradients on s.
+  const hipStream_t ws2 = p->wgrad_stream(s);
+  if (ws2 != s) {
+    HIP_TRY(hipEventRecord(p->wfork, s));
+    HIP_TRY(hipStreamWaitEvent(ws2, p->wfork, 0));
+  }
+  {
+    StageTimer tm(p, ws2, MOE_STAGE_ROUTER_BWD);
+    const int grid = ceil_div(T, 4);
+    switch (route_epl(E)) {
+      case 1: launch_router_bwd<1, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 2: launch_router_bwd<2, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 4: launch_router_bwd<4, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 8: launch_router_bwd<8, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      default: launch_router_bwd<16, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+    }
+    LAUNCH_CHECK();
+    launch_dense_wgrad<D, 1>(ws2, dlt, nullptr, Epad, x, H, T, E, H, 1.0f, (D*)g->router, nullptr,
+                             partial);
+    if (c.has_router_bias && g->router_bias) {
+      const int nrb = ceil_div(T, 64);
+      float* part = (float*)(ws);  // column partials at workspace offset 0
+      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ws2, dl, T, E,
+                         part);
+      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ws2, part, nrb, E,
+                         1.0f, g->router_bias);
+    }
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
+    const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
+    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(256), 0, ws2, dY, nullptr, (int64_t)H, A,
+                       (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
+    LAUNCH_CHECK();
+  }
   {
     StageTimer tm(p, s, MOE_STAGE_DOWN_DGRAD);
     with_row_tiling<CB, D, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
@@ -774,13 +818,18 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     });
     LAUNCH_CHECK();
   }
+  if (ws2 != s) {
+    HIP_TRY(hipEventRecord(p->wmid, s));
+    HIP_TRY(hipStreamWaitEvent(ws2, p->wmid, 0));
+  }
   {
-    StageTimer tm(p, s, MOE_STAGE_DOWN_WGRAD);
-    const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
-    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(256), 0, s, dY, nullptr, (int64_t)H, A,
-                       (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
+    StageTimer tm(p, ws2, MOE_STAGE_GATEUP_WGRAD);
+    const int grid = kgrouped_grid(E, I, H, CW::BM, CW::BN);
+    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(256), 0, ws2, dG, dU, (int64_t)I, xp,
+                       (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
+  if (ws2 != s) HIP_TRY(hipEventRecord(p->wjoin, ws2));
   {
     StageTimer tm(p, s, MOE_STAGE_GATEUP_DGRAD);
     with_row_tiling<CB, D, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
@@ -790,36 +839,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     });
     LAUNCH_CHECK();
   }
-  {
-    StageTimer tm(p, s, MOE_STAGE_GATEUP_WGRAD);
-    const int grid = kgrouped_grid(E, I, H, CW::BM, CW::BN);
-    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(256), 0, s, dG, dU, (int64_t)I, xp,
-                       (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
-    LAUNCH_CHECK();
-  }
-  {
-    StageTimer tm(p, s, MOE_STAGE_ROUTER_BWD);
-    const int grid = ceil_div(T, 4);
-    switch (route_epl(E)) {
-      case 1: launch_router_bwd<1, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      case 2: launch_router_bwd<2, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      case 4: launch_router_bwd<4, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      case 8: launch_router_bwd<8, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      default: launch_router_bwd<16, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-    }
-    LAUNCH_CHECK();
-    launch_dense_wgrad<D, 1>(s, dlt, nullptr, Epad, x, H, T, E, H, 1.0f, (D*)g->router, nullptr,
-                             partial);
-    if (c.has_router_bias && g->router_bias) {
-      const int nrb = ceil_div(T, 64);
-      float* part = (float*)(ws);  // column partials at workspace offset 0
-      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, dl, T, E,
-                         part);
-      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, s, part, nrb, E,
-                         1.0f, g->router_bias);
-    }
-    LAUNCH_CHECK();
-  }
+  if (ws2 != s) HIP_TRY(hipStreamWaitEvent(s, p->wjoin, 0));
   if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
   {
     StageTimer tm(p, s, MOE_STAGE_DX);
@@ -923,6 +943,10 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->join, hipEventDisableTiming);
   }
+  if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->wgs, hipStreamNonBlocking);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wfork, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wmid, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wjoin, hipEventDisableTiming);
   if (e != hipSuccess) {
     moe_plan_destroy(p);
     return fail(e == hipErrorOutOfMemory ? MOE_ERR_OOM : MOE_ERR_HIP, "plan set-up: %s",
@@ -945,6 +969,10 @@ moe_status moe_plan_destroy(moe_plan* p) {
   if (p->fork) (void)hipEventDestroy(p->fork);
   if (p->join) (void)hipEventDestroy(p->join);
   if (p->aux) (void)hipStreamDestroy(p->aux);
+  if (p->wgs) (void)hipStreamSynchronize(p->wgs);
+  for (hipEvent_t ev : {p->wfork, p->wmid, p->wjoin})
+    if (ev) (void)hipEventDestroy(ev);
+  if (p->wgs) (void)hipStreamDestroy(p->wgs);
   if (p->d_tab) (void)hipFree(p->d_tab);
   if (p->h_tab) (void)hipHostFree(p->h_tab);
   delete p;
