@@ -153,6 +153,8 @@ struct moe_plan {
   // The backward's routed weight gradients and the router backward need only
   // dY / dG / dU and the routing state: they run on a third stream, beside
   // the input-gradient GEMMs of the call's stream.
+  // In the forward the same stream sums the mean router probabilities (needed
+  // only by the losses) while the call's stream dispatches.
   hipStream_t wgs = nullptr;
   hipEvent_t wfork = nullptr, wmid = nullptr, wjoin = nullptr;
   bool overlap = true;
@@ -332,9 +334,11 @@ void launch_route(hipStream_t s, int grid, const float* logits, int T, int E, in
 }
 
 // Routing (from logits already in saved), losses' P statistics and dispatch.
+// side_p: the mean probabilities P may be summed on the plan's weight-gradient
+// stream; the caller then waits for p->wjoin on s before reading P.
 template <typename D>
 moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
-                       const SavedLayout& L, const WsLayout& W) {
+                       const SavedLayout& L, const WsLayout& W, bool side_p) {
   const moe_config& c = p->cfg;
   const int T = (int)T64, E = c.num_experts, k = c.experts_per_tok;
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
@@ -364,15 +368,22 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
       hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, s, idx, probs, T, E, k,
                          1.0f / (float)T, P, counts, offsets, tprefix, perm, inv);
       LAUNCH_CHECK();
+      if (side_p && p->wgrad_stream(s) != s) HIP_TRY(hipEventRecord(p->wjoin, s));
       return MOE_OK;
     }
     const int nrb = ceil_div(T, 64);
     float* part = (float*)(ws + W.colpart);
-    hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, probs, T,
+    const hipStream_t ps = side_p ? p->wgrad_stream(s) : s;
+    if (ps != s) {
+      HIP_TRY(hipEventRecord(p->wfork, s));
+      HIP_TRY(hipStreamWaitEvent(ps, p->wfork, 0));
+    }
+    hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps, probs, T,
                        E, part);
-    hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, s, part, nrb, E,
+    hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ps, part, nrb, E,
                        1.0f / (float)T, P);
     LAUNCH_CHECK();
+    if (ps != s) HIP_TRY(hipEventRecord(p->wjoin, ps));
   }
   {
     StageTimer st(p, s, MOE_STAGE_DISPATCH);
@@ -644,7 +655,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W);
+  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, true);
   if (r != MOE_OK) return r;
   if ((r = routed_fwd<D>(p, s, T, x, st, true)) != MOE_OK) return r;
   if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
@@ -656,6 +667,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                        st.w, sY, c.shared_expert_scale, T, k, H, resid, out);
     LAUNCH_CHECK();
   }
+  if (p->wgrad_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->wjoin, 0));  // P
   {
     StageTimer tm(p, s, MOE_STAGE_LOSSES);
     hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, s, st.P, st.counts, st.lse, T, E, k,
@@ -771,36 +783,13 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                        topw, T, k, H, dw, dY);
     LAUNCH_CHECK();
   }
-  // From here the router backward and the routed weight gradients run on the
-  // weight-gradient stream ws2 (they read dw, dY, A, X_perm and, after the
-  // down projection's input gradient, dG / dU), the input gradients on s.
+  // From here the routed weight gradients run on the weight-gradient stream
+  // ws2 (they read dY, A, X_perm and, after the down projection's input
+  // gradient, dG / dU); the input gradients and the router backward on s.
   const hipStream_t ws2 = p->wgrad_stream(s);
   if (ws2 != s) {
     HIP_TRY(hipEventRecord(p->wfork, s));
     HIP_TRY(hipStreamWaitEvent(ws2, p->wfork, 0));
-  }
-  {
-    StageTimer tm(p, ws2, MOE_STAGE_ROUTER_BWD);
-    const int grid = ceil_div(T, 4);
-    switch (route_epl(E)) {
-      case 1: launch_router_bwd<1, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      case 2: launch_router_bwd<2, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      case 4: launch_router_bwd<4, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      case 8: launch_router_bwd<8, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-      default: launch_router_bwd<16, D>(ws2, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
-    }
-    LAUNCH_CHECK();
-    launch_dense_wgrad<D, 1>(ws2, dlt, nullptr, Epad, x, H, T, E, H, 1.0f, (D*)g->router, nullptr,
-                             partial);
-    if (c.has_router_bias && g->router_bias) {
-      const int nrb = ceil_div(T, 64);
-      float* part = (float*)(ws);  // column partials at workspace offset 0
-      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ws2, dl, T, E,
-                         part);
-      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ws2, part, nrb, E,
-                         1.0f, g->router_bias);
-    }
-    LAUNCH_CHECK();
   }
   {
     StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
@@ -837,6 +826,29 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
       hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(mt * ceil_div(H, C::BN)), dim3(256), 0,
                          s, dG, dU, r, tg, nullptr, tu, nullptr, I, H, dXp);
     });
+    LAUNCH_CHECK();
+  }
+  {
+    StageTimer tm(p, s, MOE_STAGE_ROUTER_BWD);
+    const int grid = ceil_div(T, 4);
+    switch (route_epl(E)) {
+      case 1: launch_router_bwd<1, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 2: launch_router_bwd<2, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 4: launch_router_bwd<4, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      case 8: launch_router_bwd<8, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+      default: launch_router_bwd<16, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
+    }
+    LAUNCH_CHECK();
+    launch_dense_wgrad<D, 1>(s, dlt, nullptr, Epad, x, H, T, E, H, 1.0f, (D*)g->router, nullptr,
+                             partial);
+    if (c.has_router_bias && g->router_bias) {
+      const int nrb = ceil_div(T, 64);
+      float* part = (float*)(ws);  // column partials at workspace offset 0
+      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, dl, T, E,
+                         part);
+      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, s, part, nrb, E,
+                         1.0f, g->router_bias);
+    }
     LAUNCH_CHECK();
   }
   if (ws2 != s) HIP_TRY(hipStreamWaitEvent(s, p->wjoin, 0));
@@ -1224,8 +1236,8 @@ moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const flo
   HIP_TRY(hipMemcpyAsync(sv + L.f[MOE_SAVED_LOGITS], logits,
                          sizeof(float) * (size_t)T * p->cfg.num_experts, hipMemcpyDeviceToDevice,
                          s));
-  if (p->cfg.dtype == MOE_DTYPE_BF16) return run_routing<bf16_t>(p, s, T, sv, (char*)workspace, L, W);
-  return run_routing<float>(p, s, T, sv, (char*)workspace, L, W);
+  if (p->cfg.dtype == MOE_DTYPE_BF16) return run_routing<bf16_t>(p, s, T, sv, (char*)workspace, L, W, false);
+  return run_routing<float>(p, s, T, sv, (char*)workspace, L, W, false);
 }
 
 const char* moe_stage_name(int32_t stage) {
