@@ -1312,7 +1312,7 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
   }
 }
 
-// Router logits for T <= kSkinnyMaxTokens (bf16): workgroup (x, y) owns 16
+// Router logits with few experts or few tokens (bf16): a workgroup owns 16
 // experts and 16 tokens; its kRouterWaves waves take every kRouterWaves-th
 // 256-wide k-chunk of the hidden dimension (same lane layout as k_skinny_fwd)
 // and the partial sums are added through LDS in wave order.  With few experts
@@ -1326,7 +1326,8 @@ __global__ __launch_bounds__(64 * kRouterWaves) void k_router_small(const bf16_t
                                                       float* __restrict__ logits, int Tn, int H,
                                                       int E) {
   __shared__ f32x4 red[kRouterWaves][64];
-  const int e0 = blockIdx.x * 16, t0 = blockIdx.y * 16;
+  const int neb = (E + 15) / 16;
+  const int e0 = uni(blockIdx.x % neb) * 16, t0 = uni(blockIdx.x / neb) * 16;
   const int wave = uni(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int g = lane >> 4, rl = lane & 15;
   const int nrows = min(16, E - e0), ntok = min(16, Tn - t0);

@@ -531,6 +531,11 @@ void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t 
     ceil_div(TK, CDEF::BM) + E);
 }
 
+// The router GEMM has N = E: up to this many experts the 16 x 16 blocks of
+// k_router_small fill the GPU better than 128 x 128 tiles (config 2, E = 16:
+// 31 -> 12 us; at E = 64 the tiles are faster).
+constexpr int kRouterSmallMaxExperts = 32;
+
 // Routed experts forward on stream s: gather X_perm, then G, U (when kept),
 // A and the per-assignment expert outputs Y.  `timed`: record the stages.
 template <typename D>
@@ -643,8 +648,8 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
-    if (std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens) {
-      hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16), ceil_div(T, 16)),
+    if (std::is_same<D, bf16_t>::value && (T <= kSkinnyMaxTokens || E <= kRouterSmallMaxExperts)) {
+      hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16) * ceil_div(T, 16)),
                          dim3(64 * kRouterWaves), 0, s, (const bf16_t*)x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
                          st.logits, T, H, E);
