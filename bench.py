@@ -362,6 +362,24 @@ def main():
         roof["kernel"] = (f"k_gateup_fwd<{'bf16' if wl.dtype == 'bf16' else 'f32'}, true> "
                           f"(grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch")
 
+    # memory-bound stages against the HBM roofline: algorithmic bytes per call
+    # (b = element size) over the serial stage time of the profiling steps
+    b = 2 if wl.dtype == "bf16" else 4
+    stage_bytes = {
+        "router_gemm": T * H * b + E * H * b + T * E * 4,
+        "route": 3 * T * E * 4 + T * 4 + TK * 8,
+        "dispatch": 2 * TK * 4 + TK * 8 + 2 * E * 4,
+        "gather": T * H * b + TK * H * b + TK * 4,
+        "combine_fwd": TK * H * b + (T * H * b if S else 0) + TK * 8 + T * H * b,
+    }
+    if wl.backward:
+        stage_bytes["combine_bwd"] = T * H * b + 2 * TK * H * b + TK * 8 + TK * 4
+    hbm_stages = {}
+    for name, nbytes in stage_bytes.items():
+        if stages.get(name):
+            gbs = nbytes / (stages[name] * 1e-3) / 1e9
+            hbm_stages[name] = {"GB/s": round(gbs, 1), "frac": round(gbs / PEAK_HBM_GBS, 4)}
+
     gemm_stages = ("gateup_fwd", "down_fwd", "shared_fwd", "down_dgrad", "down_wgrad",
                    "gateup_dgrad", "gateup_wgrad", "shared_bwd", "router_gemm", "dx")
     gemm_ms = sum(stages.get(s, 0.0) for s in gemm_stages)
@@ -388,6 +406,7 @@ def main():
         "layer_mfma_frac": round(total_flops / (elapsed / args.steps) / 1e12 / peak, 4),
         "gemm_tflops": round(total_flops / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
         "stages_ms": {n: round(v, 4) for n, v in stages.items()},
+        "hbm_stages": hbm_stages,
         **extra,
     }
     if args.cpu_baseline == "on":
