@@ -192,15 +192,18 @@ def test_bitwise_reproducible(dtype):
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
 
 
-@pytest.mark.parametrize("dtype", ["f32", "bf16"])
-def test_shared_stream_overlap_is_bitwise_serial(dtype):
-    # the shared expert on the plan's second stream gives the same bits as the
-    # serial order: no result depends on how the two streams interleave
-    case = Case(T=640, H=128, E=16, k=2, I=64, S=128, dtype=dtype, w_std=0.05, seed=5)
+@pytest.mark.parametrize("dtype,S", [("f32", 128), ("bf16", 128), ("bf16", 0)])
+def test_shared_stream_overlap_is_bitwise_serial(dtype, S):
+    # the shared expert on the plan's second stream and the weight gradients
+    # (and the forward's mean probabilities) on its third give the same bits
+    # as the serial order: no result depends on how the streams interleave
+    case = Case(T=640, H=128, E=16, k=2, I=64, S=S, dtype=dtype, w_std=0.05, seed=5)
     a = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=True)
     b = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=False)
-    for n in ("out", "aux", "z", "dx", "router", "gate", "up", "down", "shared_gate",
-              "shared_up", "shared_down"):
+    names = ["out", "aux", "z", "dx", "router", "gate", "up", "down"]
+    if S:
+        names += ["shared_gate", "shared_up", "shared_down"]
+    for n in names:
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
 
 
