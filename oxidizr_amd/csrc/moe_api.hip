@@ -297,6 +297,36 @@ struct StageTimer {
   }
 };
 
+// Work forked from the call's stream s onto a side stream of the plan is
+// joined back with `ev`: join() records ev on the side stream and makes s wait
+// for it.  A fork that is not joined explicitly (an error return in between)
+// is joined when the guard goes out of scope, so no side-stream work is ever
+// left unordered with the caller's stream.
+struct SideJoin {
+  hipStream_t s = nullptr, side = nullptr;
+  hipEvent_t ev = nullptr;
+  bool armed = false;
+  // fork: side waits for everything enqueued on s so far (fork_ev)
+  hipError_t fork(hipStream_t s_, hipStream_t side_, hipEvent_t fork_ev, hipEvent_t join_ev) {
+    s = s_;
+    side = side_;
+    ev = join_ev;
+    if (side == s) return hipSuccess;
+    hipError_t e = hipEventRecord(fork_ev, s);
+    if (e == hipSuccess) e = hipStreamWaitEvent(side, fork_ev, 0);
+    armed = e == hipSuccess;
+    return e;
+  }
+  hipError_t join() {
+    if (!armed) return hipSuccess;
+    armed = false;
+    hipError_t e = hipEventRecord(ev, side);
+    if (e == hipSuccess) e = hipStreamWaitEvent(s, ev, 0);
+    return e;
+  }
+  ~SideJoin() { (void)join(); }
+};
+
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 moe_status upload_tables(moe_plan* p, hipStream_t s, int first, const void* const* tabs[3]) {
@@ -334,11 +364,12 @@ void launch_route(hipStream_t s, int grid, const float* logits, int T, int E, in
 }
 
 // Routing (from logits already in saved), losses' P statistics and dispatch.
-// side_p: the mean probabilities P may be summed on the plan's weight-gradient
-// stream; the caller then waits for p->wjoin on s before reading P.
+// pjoin != null: the mean probabilities P may be summed on the plan's
+// weight-gradient stream, forked through *pjoin; the caller joins it before
+// reading P.
 template <typename D>
 moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
-                       const SavedLayout& L, const WsLayout& W, bool side_p) {
+                       const SavedLayout& L, const WsLayout& W, SideJoin* pjoin) {
   const moe_config& c = p->cfg;
   const int T = (int)T64, E = c.num_experts, k = c.experts_per_tok;
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
@@ -368,22 +399,17 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
       hipLaunchKernelGGL(k_dispatch_small, dim3(1), dim3(1024), 0, s, idx, probs, T, E, k,
                          1.0f / (float)T, P, counts, offsets, tprefix, perm, inv);
       LAUNCH_CHECK();
-      if (side_p && p->wgrad_stream(s) != s) HIP_TRY(hipEventRecord(p->wjoin, s));
       return MOE_OK;
     }
     const int nrb = ceil_div(T, 64);
     float* part = (float*)(ws + W.colpart);
-    const hipStream_t ps = side_p ? p->wgrad_stream(s) : s;
-    if (ps != s) {
-      HIP_TRY(hipEventRecord(p->wfork, s));
-      HIP_TRY(hipStreamWaitEvent(ps, p->wfork, 0));
-    }
+    const hipStream_t ps = pjoin ? p->wgrad_stream(s) : s;
+    if (pjoin) HIP_TRY(pjoin->fork(s, ps, p->wfork, p->wjoin));
     hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps, probs, T,
                        E, part);
     hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ps, part, nrb, E,
                        1.0f / (float)T, P);
     LAUNCH_CHECK();
-    if (ps != s) HIP_TRY(hipEventRecord(p->wjoin, ps));
   }
   {
     StageTimer st(p, s, MOE_STAGE_DISPATCH);
@@ -634,17 +660,14 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const State<D> st(rb, LR, ab, keep_act ? LR : LT);
   // Shared expert first, on the plan's second stream: it only needs x.
   D* sY = nullptr;
+  SideJoin shared_join, p_join;
   if (S > 0) {
     const hipStream_t ss = p->shared_stream(s);
-    if (ss != s) {
-      HIP_TRY(hipEventRecord(p->fork, s));
-      HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
-    }
+    HIP_TRY(shared_join.fork(s, ss, p->fork, p->join));
     StageTimer tm(p, ss, MOE_STAGE_SHARED_FWD);
     sY = (D*)(ws + W.sY);
     shared_fwd<D>(p, ss, T, x, w, st.sG, st.sU, st.sA, sY);
     LAUNCH_CHECK();
-    if (ss != s) HIP_TRY(hipEventRecord(p->join, ss));
   }
   {
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
@@ -660,10 +683,10 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, true);
+  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join);
   if (r != MOE_OK) return r;
   if ((r = routed_fwd<D>(p, s, T, x, st, true)) != MOE_OK) return r;
-  if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
+  HIP_TRY(shared_join.join());
   {
     StageTimer tm(p, s, MOE_STAGE_COMBINE_FWD);
     const int nsl = ceil_div(H / (16 / (int)sizeof(D)), kCombineSlice);
@@ -672,7 +695,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                        st.w, sY, c.shared_expert_scale, T, k, H, resid, out);
     LAUNCH_CHECK();
   }
-  if (p->wgrad_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->wjoin, 0));  // P
+  HIP_TRY(p_join.join());  // P
   {
     StageTimer tm(p, s, MOE_STAGE_LOSSES);
     hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, s, st.P, st.counts, st.lse, T, E, k,
@@ -746,12 +769,10 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   // Shared expert backward first, on the plan's second stream: it needs only
   // d_out, x and its own saved activations; dx waits for it below.
   D* dxs = nullptr;
+  SideJoin shared_join, wgrad_join;
   if (S > 0) {
     const hipStream_t ss = p->shared_stream(s);
-    if (ss != s) {
-      HIP_TRY(hipEventRecord(p->fork, s));
-      HIP_TRY(hipStreamWaitEvent(ss, p->fork, 0));
-    }
+    HIP_TRY(shared_join.fork(s, ss, p->fork, p->join));
     if (recompute) {
       StageTimer tm(p, ss, MOE_STAGE_RECOMPUTE);
       shared_fwd<D>(p, ss, T, x, w, st.sG, st.sU, st.sA, nullptr);
@@ -776,7 +797,6 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     launch_dense_wgrad<D, 2>(ss, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
                              (D*)g->shared_up, partial_sh);
     LAUNCH_CHECK();
-    if (ss != s) HIP_TRY(hipEventRecord(p->join, ss));
   }
   if (recompute) {
     moe_status r = routed_fwd<D>(p, s, T, x, st, false);
@@ -792,10 +812,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   // ws2 (they read dY, A, X_perm and, after the down projection's input
   // gradient, dG / dU); the input gradients and the router backward on s.
   const hipStream_t ws2 = p->wgrad_stream(s);
-  if (ws2 != s) {
-    HIP_TRY(hipEventRecord(p->wfork, s));
-    HIP_TRY(hipStreamWaitEvent(ws2, p->wfork, 0));
-  }
+  HIP_TRY(wgrad_join.fork(s, ws2, p->wfork, p->wjoin));
   {
     StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
     const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
@@ -823,7 +840,6 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                        (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
-  if (ws2 != s) HIP_TRY(hipEventRecord(p->wjoin, ws2));
   {
     StageTimer tm(p, s, MOE_STAGE_GATEUP_DGRAD);
     with_row_tiling<CB, D, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
@@ -856,8 +872,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     }
     LAUNCH_CHECK();
   }
-  if (ws2 != s) HIP_TRY(hipStreamWaitEvent(s, p->wjoin, 0));
-  if (S > 0 && p->shared_stream(s) != s) HIP_TRY(hipStreamWaitEvent(s, p->join, 0));
+  HIP_TRY(wgrad_join.join());
+  HIP_TRY(shared_join.join());
   {
     StageTimer tm(p, s, MOE_STAGE_DX);
     hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, CR::BM) * ceil_div(H, CR::BN)),
@@ -1241,8 +1257,8 @@ moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const flo
   HIP_TRY(hipMemcpyAsync(sv + L.f[MOE_SAVED_LOGITS], logits,
                          sizeof(float) * (size_t)T * p->cfg.num_experts, hipMemcpyDeviceToDevice,
                          s));
-  if (p->cfg.dtype == MOE_DTYPE_BF16) return run_routing<bf16_t>(p, s, T, sv, (char*)workspace, L, W, false);
-  return run_routing<float>(p, s, T, sv, (char*)workspace, L, W, false);
+  if (p->cfg.dtype == MOE_DTYPE_BF16) return run_routing<bf16_t>(p, s, T, sv, (char*)workspace, L, W, nullptr);
+  return run_routing<float>(p, s, T, sv, (char*)workspace, L, W, nullptr);
 }
 
 const char* moe_stage_name(int32_t stage) {
