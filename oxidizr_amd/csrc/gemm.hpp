@@ -23,14 +23,19 @@
 
 namespace moe {
 
-template <typename T, int BM_, int BN_, int BK_>
+// BM x BN output tile per workgroup of 4 waves arranged WGM x WGN (wave w
+// owns block (w / WGN, w % WGN)), BK-deep k-tiles.
+template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2>
 struct Tiling {
   static constexpr int BM = BM_, BN = BN_, BK = BK_;
   static constexpr int V = Vec16<T>::N;   // elements per 16-byte vector
   static constexpr int LDK = BK + V;      // padded LDS row pitch (elements)
   static constexpr int THREADS = 256;
-  static constexpr int WM = BM / 2, WN = BN / 2;  // per-wave tile
+  static constexpr int WGN = WGN_, WGM = 4 / WGN_;  // wave grid
+  static constexpr int WM = BM / WGM, WN = BN / WGN;  // per-wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA blocks per wave
+  static_assert(WGM * WGN == 4, "four waves");
+  static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tiles of whole 32 x 32 blocks");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % (2 * V) == 0, "BK must cover whole MFMA k-steps");
 };
@@ -322,7 +327,7 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
   using SB = typename std::conditional<B_T, DmaStagerT<C, T, C::BN>, DmaStager<C, T, C::BN>>::type;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
   SA sa[NA];
   SB sb[NB];
   const int nk1 = (K + C::BK - 1) / C::BK;
@@ -445,7 +450,7 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
   constexpr int B_OFF = NA * C::BM * C::LDK;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
   Stager<C, T, C::BM, A_T> sa[NA];
   Stager<C, T, C::BN, B_T> sb[NB];
   const int nk1 = (K + C::BK - 1) / C::BK;
@@ -551,7 +556,7 @@ MOE_DEV void zero_acc(f32x16 (&acc)[NACC][C::TN][C::TM]) {
 template <class C, int NACC, class F>
 MOE_DEV void for_each_frag(const f32x16 (&acc)[NACC][C::TN][C::TM], F&& f) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
 #pragma unroll
   for (int tn = 0; tn < C::TN; ++tn)
 #pragma unroll
@@ -605,7 +610,7 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
   constexpr int NQ = NPRE > 0 ? NPRE : 1;
   constexpr int RG = C::WM / 16;  // row groups of a block
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
   float* reg = lds + wave * NACC * C::WM * P;
 #pragma unroll
   for (int tn = 0; tn < C::TN; ++tn) {  // unrolled: acc is indexed by constants only

@@ -571,34 +571,69 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // separate instantiation, so profiles tell the two launches apart).
 // C: the tiling (Tilings<T>::GateUp, or 128-row tiles for experts with few
 // rows, whose last row tile would otherwise be mostly padding).
+// Row-grouped tiles whose group leaves at most half of the BM rows valid (the
+// last tile of an expert) run as a BM/2-row tile with the four waves side by
+// side along N (HalfRows<C>), so every wave multiplies valid rows and the tile
+// takes about half the time; the per-element k order is unchanged, so the
+// results are the same bits.  bf16 256-row tiles only.
+template <class C>
+using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4>;
+template <typename T, class C>
+constexpr bool has_half_rows() { return sizeof(T) == 2 && C::BM == 256; }
+template <typename T, class C, int NA, int NB, int NACC>
+constexpr int rowgroup_smem_elems() {
+  if constexpr (has_half_rows<T, C>()) {
+    constexpr int a = kernel_smem_elems<C, T, NA, NB, NACC>();
+    constexpr int b = kernel_smem_elems<HalfRows<C>, T, NA, NB, NACC>();
+    return a > b ? a : b;
+  } else {
+    return kernel_smem_elems<C, T, NA, NB, NACC>();
+  }
+}
+// Runs body(tiling) for a resolved row tile: the half-height tiling when the
+// tile has at most BM / 2 valid rows.
+template <typename T, class C, class F>
+MOE_DEV void with_tile_rows(int mv, F&& body) {
+  if constexpr (has_half_rows<T, C>()) {
+    if (mv <= C::BM / 2) {
+      body(HalfRows<C>{});
+      return;
+    }
+  }
+  body(C{});
+}
+
 template <typename T, bool GROUPED, class C = typename Tilings<T>::GateUp>
 __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
                                                     const T* const* wg_tab, const T* wg_one,
                                                     const T* const* wu_tab, const T* wu_one,
                                                     int H, int N, T* __restrict__ G,
                                                     T* __restrict__ U, T* __restrict__ A) {
-  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 2, 2>()];
+  __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 2, 2>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);
   const T* wu = pick(wu_tab, wu_one, grp);
-  OpDesc<T> a[1] = {{X + (int64_t)row0 * H, H, mv, H}};
-  OpDesc<T> b[2] = {{wg + (int64_t)n0 * H, H, N - n0, H}, {wu + (int64_t)n0 * H, H, N - n0, H}};
-  f32x16 acc[2][C::TN][C::TM];
-  zero_acc<C, 2>(acc);
-  mainloop<C, T, false, false, 1, 2>(acc, a, b, H, smem);
-  static_assert(epi_lds_floats<C, 2>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-  for_each_row8<C, 2>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
-    if (m >= mv || n0 + n >= N) return;
-    float act[8];
+  with_tile_rows<T, C>(mv, [&](auto ct) {
+    using CT = decltype(ct);
+    OpDesc<T> a[1] = {{X + (int64_t)row0 * H, H, mv, H}};
+    OpDesc<T> b[2] = {{wg + (int64_t)n0 * H, H, N - n0, H}, {wu + (int64_t)n0 * H, H, N - n0, H}};
+    f32x16 acc[2][CT::TN][CT::TM];
+    zero_acc<CT, 2>(acc);
+    mainloop<CT, T, false, false, 1, 2>(acc, a, b, H, smem);
+    static_assert(epi_lds_floats<CT, 2>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+    for_each_row8<CT, 2>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+      if (m >= mv || n0 + n >= N) return;
+      float act[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) act[i] = silu_f(v[0][i]) * v[1][i];
-    const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
-    if (G) {  // pre-activations are kept only for a backward
-      store8(G + o, v[0]);
-      store8(U + o, v[1]);
-    }
-    store8(A + o, act);
+      for (int i = 0; i < 8; ++i) act[i] = silu_f(v[0][i]) * v[1][i];
+      const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
+      if (G) {  // pre-activations are kept only for a backward
+        store8(G + o, v[0]);
+        store8(U + o, v[1]);
+      }
+      store8(A + o, act);
+    });
   });
 }
 
@@ -607,19 +642,22 @@ template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
                                                   const T* const* wd_tab, const T* wd_one, int I,
                                                   int H, T* __restrict__ Y) {
-  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
+  __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);
-  OpDesc<T> a[1] = {{A + (int64_t)row0 * I, I, mv, I}};
-  OpDesc<T> b[1] = {{wd + (int64_t)n0 * I, I, H - n0, I}};
-  f32x16 acc[1][C::TN][C::TM];
-  zero_acc<C, 1>(acc);
-  mainloop<C, T, false, false, 1, 1>(acc, a, b, I, smem);
-  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
-    if (m >= mv || n0 + n >= H) return;
-    store8(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+  with_tile_rows<T, C>(mv, [&](auto ct) {
+    using CT = decltype(ct);
+    OpDesc<T> a[1] = {{A + (int64_t)row0 * I, I, mv, I}};
+    OpDesc<T> b[1] = {{wd + (int64_t)n0 * I, I, H - n0, I}};
+    f32x16 acc[1][CT::TN][CT::TM];
+    zero_acc<CT, 1>(acc);
+    mainloop<CT, T, false, false, 1, 1>(acc, a, b, I, smem);
+    static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+    for_each_row8<CT, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+      if (m >= mv || n0 + n >= H) return;
+      store8(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+    });
   });
 }
 
@@ -735,16 +773,10 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
                                                     const T* __restrict__ G,
                                                     const T* __restrict__ U,
                                                     T* __restrict__ dG, T* __restrict__ dU) {
-  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
+  __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);  // [H, N]: element (n, k=h) at wd + h*N + n
-  OpDesc<T> a[1] = {{dY + (int64_t)row0 * H, H, mv, H}};
-  OpDesc<T> b[1] = {{wd + n0, N, N - n0, H}};
-  f32x16 acc[1][C::TN][C::TM];
-  zero_acc<C, 1>(acc);
-  mainloop<C, T, false, true, 1, 1>(acc, a, b, H, smem);
-  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
   // G and U of a whole 32-column block are requested before its rows are
   // visited; rows outside the tile read zeros (out-of-range offsets)
   constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
@@ -759,25 +791,34 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
       q[NV + j] = buf_ld16(ru, off + 16 * j, 0);
     }
   };
-  for_each_row8_pre<C, 1, 2 * NV>(acc, reinterpret_cast<float*>(smem), pre,
-                                  [&](int m, int n, auto& v, const u32x4 (&q)[2 * NV]) {
-    if (m >= mv || n0 + n >= N) return;
-    const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
-    float g[8], u[8], dg[8], du[8];
+  with_tile_rows<T, C>(mv, [&](auto ct) {
+    using CT = decltype(ct);
+    OpDesc<T> a[1] = {{dY + (int64_t)row0 * H, H, mv, H}};
+    OpDesc<T> b[1] = {{wd + n0, N, N - n0, H}};
+    f32x16 acc[1][CT::TN][CT::TM];
+    zero_acc<CT, 1>(acc);
+    mainloop<CT, T, false, true, 1, 1>(acc, a, b, H, smem);
+    static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+    for_each_row8_pre<CT, 1, 2 * NV>(acc, reinterpret_cast<float*>(smem), pre,
+                                     [&](int m, int n, auto& v, const u32x4 (&q)[2 * NV]) {
+      if (m >= mv || n0 + n >= N) return;
+      const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
+      float g[8], u[8], dg[8], du[8];
 #pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      unpack16(q[j], g + j * (8 / NV), T());
-      unpack16(q[NV + j], u + j * (8 / NV), T());
-    }
+      for (int j = 0; j < NV; ++j) {
+        unpack16(q[j], g + j * (8 / NV), T());
+        unpack16(q[NV + j], u + j * (8 / NV), T());
+      }
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float da = alpha * v[0][i];
-      const float sg = sigmoid_f(g[i]);
-      dg[i] = da * u[i] * (sg * (1.0f + g[i] * (1.0f - sg)));
-      du[i] = da * (g[i] * sg);
-    }
-    store8(dG + o, dg);
-    store8(dU + o, du);
+      for (int i = 0; i < 8; ++i) {
+        const float da = alpha * v[0][i];
+        const float sg = sigmoid_f(g[i]);
+        dg[i] = da * u[i] * (sg * (1.0f + g[i] * (1.0f - sg)));
+        du[i] = da * (g[i] * sg);
+      }
+      store8(dG + o, dg);
+      store8(dU + o, du);
+    });
   });
 }
 
@@ -788,23 +829,26 @@ __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
                                                       const T* const* wg_tab, const T* wg_one,
                                                       const T* const* wu_tab, const T* wu_one,
                                                       int I, int H, T* __restrict__ dX) {
-  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
+  __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);  // [I, H]: element (n=h, k=i) at wg + i*H + h
   const T* wu = pick(wu_tab, wu_one, grp);
-  f32x16 acc[1][C::TN][C::TM];
-  zero_acc<C, 1>(acc);
-  // one pipelined loop over K = 2I: the dG / Wg segment, then dU / Wu
-  OpDesc<T> a[1] = {{dG + (int64_t)row0 * I, I, mv, I}};
-  OpDesc<T> b[1] = {{wg + n0, H, H - n0, I}};
-  OpDesc<T> a2[1] = {{dU + (int64_t)row0 * I, I, mv, I}};
-  OpDesc<T> b2[1] = {{wu + n0, H, H - n0, I}};
-  mainloop<C, T, false, true, 1, 1>(acc, a, b, I, smem, a2, b2, I);
-  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
-    if (m >= mv || n0 + n >= H) return;
-    store8(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+  with_tile_rows<T, C>(mv, [&](auto ct) {
+    using CT = decltype(ct);
+    f32x16 acc[1][CT::TN][CT::TM];
+    zero_acc<CT, 1>(acc);
+    // one pipelined loop over K = 2I: the dG / Wg segment, then dU / Wu
+    OpDesc<T> a[1] = {{dG + (int64_t)row0 * I, I, mv, I}};
+    OpDesc<T> b[1] = {{wg + n0, H, H - n0, I}};
+    OpDesc<T> a2[1] = {{dU + (int64_t)row0 * I, I, mv, I}};
+    OpDesc<T> b2[1] = {{wu + n0, H, H - n0, I}};
+    mainloop<CT, T, false, true, 1, 1>(acc, a, b, I, smem, a2, b2, I);
+    static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+    for_each_row8<CT, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+      if (m >= mv || n0 + n >= H) return;
+      store8(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+    });
   });
 }
 
