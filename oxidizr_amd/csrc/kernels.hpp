@@ -345,8 +345,8 @@ __global__ __launch_bounds__(256) void k_hist(const int* __restrict__ idx, int T
 
 // counts, exclusive offsets, per-block bases, and GEMM tile prefixes for the
 // row-tile heights in kTileBM.
-constexpr int kNumTileBM = 5;
-__constant__ int kTileBM[kNumTileBM] = {16, 32, 64, 128, 256};
+constexpr int kNumTileBM = 2;
+__constant__ int kTileBM[kNumTileBM] = {128, 256};
 
 // Inclusive prefix sum across the 64 lanes of a wave.
 MOE_DEV int wave_incl_scan(int v) {

@@ -425,11 +425,10 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
   return MOE_OK;
 }
 
-int tile_slot(int bm) {
-  switch (bm) {
-    case 16: return 0; case 32: return 1; case 64: return 2; case 128: return 3; default: return 4;
-  }
-}
+// Index of a row-tile height in kTileBM (the row-grouped tilings use 128
+// (fp32) and 256 (bf16) rows).
+constexpr int tile_slot(int bm) { return bm == 128 ? 0 : 1; }
+static_assert(kNumTileBM == 2, "tile_slot covers the heights of kTileBM");
 
 // Blocks of a K-grouped (weight-gradient) launch over `groups` groups or
 // split chunks of an M x N output: each takes 8 * ceil(tiles / 8) blocks.
@@ -530,31 +529,12 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   }
 }
 
-// Experts hold few rows on average (fewer than two 256-row tiles): 128-row
-// tiles waste less of the last tile of each expert.
-constexpr int kSmallRowsPerExpert = 512;
-template <typename D>
-bool small_rows(int64_t TK, int E) {
-  return sizeof(D) == 2 && TK < (int64_t)kSmallRowsPerExpert * E;
-}
-
-// Calls f(tiling, row groups, row-tile count) for a row-grouped launch: the
-// default tiling CDEF, or (SMALL_OK, bf16) 128-row tiles when experts hold few
-// rows.  Measured on config 5 (~256 rows per expert): the gate/up forward
-// (two B operands, 128 x 512 outputs per workgroup) gains 6 %; the
-// single-operand GEMMs lose 8-15 % with 128 x 256 tiles, so they keep 256 rows.
-template <class CDEF, typename D, bool SMALL_OK, class F>
+// Calls f(tiling, row groups, row-tile upper bound) for a row-grouped launch
+// of tiling C: the tile-prefix table of C::BM and the grid bound TK/BM + E.
+template <class C, class F>
 void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t TK, F&& f) {
-  if constexpr (sizeof(D) == 2 && SMALL_OK) {
-    if (small_rows<D>(TK, E)) {
-      using CS = Tiling<bf16_t, 128, CDEF::BN == 128 ? 256 : CDEF::BN, 64>;
-      f(CS{}, RowGroups{offsets, tprefix_all + tile_slot(CS::BM) * (E + 1), E, (int)TK},
-        ceil_div(TK, CS::BM) + E);
-      return;
-    }
-  }
-  f(CDEF{}, RowGroups{offsets, tprefix_all + tile_slot(CDEF::BM) * (E + 1), E, (int)TK},
-    ceil_div(TK, CDEF::BM) + E);
+  f(C{}, RowGroups{offsets, tprefix_all + tile_slot(C::BM) * (E + 1), E, (int)TK},
+    ceil_div(TK, C::BM) + E);
 }
 
 // The router GEMM has N = E: up to this many experts the 16 x 16 blocks of
@@ -604,7 +584,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
                            nullptr, (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G,
                            (bf16_t*)st.U, (bf16_t*)st.A);
     } else {
-      with_row_tiling<CG, D, true>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+      with_row_tiling<CG>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
         using C = decltype(c);
         hipLaunchKernelGGL((k_gateup_fwd<D, true, C>), dim3(mt * ceil_div(I, C::BN)), dim3(256), 0,
                            s, st.xp, r, tg, nullptr, tu, nullptr, H, I, st.G, st.U, st.A);
@@ -623,7 +603,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
                            s, (const bf16_t*)st.A, nullptr, 1, 0, st.offsets, E, 0, (const bf16_t* const*)td,
                            nullptr, nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
     } else {
-      with_row_tiling<CB, D, false>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+      with_row_tiling<CB>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
         using C = decltype(c);
         hipLaunchKernelGGL((k_down_fwd<D, true, C>), dim3(mt * ceil_div(H, C::BN)), dim3(256), 0, s,
                            st.A, r, td, nullptr, I, H, st.Y);
@@ -822,7 +802,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_DOWN_DGRAD);
-    with_row_tiling<CB, D, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+    with_row_tiling<CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
       using C = decltype(c);
       hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(mt * ceil_div(I, C::BN)), dim3(256), 0, s,
                          dY, r, td, nullptr, H, I, 1.0f, G, U, dG, dU);
@@ -842,7 +822,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_GATEUP_DGRAD);
-    with_row_tiling<CB, D, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+    with_row_tiling<CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
       using C = decltype(c);
       hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(mt * ceil_div(H, C::BN)), dim3(256), 0,
                          s, dG, dU, r, tg, nullptr, tu, nullptr, I, H, dXp);
