@@ -117,3 +117,27 @@ MOE_DEV bool xcd_slot(int b, int n, int& id) {
   id = x * q + (x < r ? x : r) + j;
   return true;
 }
+
+// Two classes of tiles, n0 of class 0 and n1 of class 1, dealt over the 8
+// XCDs: each XCD receives a contiguous range of each class (neighbouring
+// tiles share its L2) and runs its class-0 tiles before its class-1 tiles.
+// The class-1 remainder starts at the XCD after the last class-0 remainder,
+// so no XCD holds more than ceil((n0 + n1) / 8) tiles.  Needs a grid of at
+// least 8 * ceil((n0 + n1) / 8) blocks; returns false for blocks past their
+// XCD's tiles.
+MOE_DEV bool xcd_slot2(int b, int n0, int n1, int& cls, int& id) {
+  const int x = b & 7, j = b >> 3;
+  const int q0 = n0 >> 3, r0 = n0 & 7, q1 = n1 >> 3, r1 = n1 & 7;
+  const int c0 = q0 + (x < r0 ? 1 : 0);
+  if (j < c0) {
+    cls = 0;
+    id = x * q0 + (x < r0 ? x : r0) + j;
+    return true;
+  }
+  const int xr = (x - r0) & 7;  // rank of this XCD in the class-1 dealing
+  const int j1 = j - c0;
+  if (j1 >= q1 + (xr < r1 ? 1 : 0)) return false;
+  cls = 1;
+  id = xr * q1 + (xr < r1 ? xr : r1) + j1;
+  return true;
+}

@@ -40,11 +40,21 @@ template <> struct Tilings<float> {
 
 // Row-grouped problems: groups split the M dimension (permuted token rows).
 // offsets == nullptr means one dense group of M rows.
+// A group of c rows has c / BM full row tiles and, when r = c % BM is not 0, a
+// last tile of r rows.  That tile counts among the "big" tiles when r > BM / 2
+// and is a "half" tile otherwise.  Tiles run group by group (a group's tiles
+// share its weight panels in L2), or, with half_last, every half tile after
+// every big tile: the half-height tiles then fill the last round of the launch
+// instead of adding a round among the big tiles, at the cost of reading their
+// group's weights once more.
 struct RowGroups {
   const int* offsets;      // [G + 1] row offsets
-  const int* tile_prefix;  // [G + 1] prefix of ceil(count / BM)
+  const int* tile_prefix;  // [G + 1] prefix of the row tiles: ceil(c / BM)
+  const int* big_prefix;   // [G + 1] prefix of the big row tiles: c / BM + (r > BM / 2)
+  const int* half_prefix;  // [G + 1] prefix of the half row tiles: 0 < r <= BM / 2
   int G;
   int M;                   // rows in all groups (the extent of row-major operands)
+  int half_last;
 };
 
 // Tile coordinates are workgroup-uniform, but integer division by a runtime
@@ -68,23 +78,41 @@ MOE_DEV bool tile_order(int id, int nM, int nN, int& mt, int& nt) {
   return nt < nN;
 }
 
+// Row-grouped launches need a grid of at least 8 * ceil(tiles / 8) blocks
+// (xcd_slot2); dense ones at least the tile count.
 MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, int& row0,
                           int& mv, int& n0) {
   const int nN = (N + BN - 1) / BN;
-  const int nM = g.offsets == nullptr ? (g.M + BM - 1) / BM : g.tile_prefix[g.G];
   int id, mt, nt;
-  if (!xcd_slot(blockIdx.x, nM * nN, id) || !tile_order(id, nM, nN, mt, nt)) return false;
-  n0 = nt * BN;
   if (g.offsets == nullptr) {
+    const int nM = (g.M + BM - 1) / BM;
+    if (!xcd_slot(blockIdx.x, nM * nN, id) || !tile_order(id, nM, nN, mt, nt)) return false;
+    n0 = nt * BN;
     grp = 0;
     row0 = mt * BM;
     mv = min(BM, g.M - row0);
     return mv > 0;
   }
-  grp = uni(find_group(g.tile_prefix, g.G, mt));
-  const int local = (mt - g.tile_prefix[grp]) * BM;
+  int local;
+  if (g.half_last) {
+    const int nB = g.big_prefix[g.G], nH = g.half_prefix[g.G];
+    int cls;
+    if (!xcd_slot2(blockIdx.x, nB * nN, nH * nN, cls, id)) return false;
+    const int* pre = cls ? g.half_prefix : g.big_prefix;
+    if (!tile_order(id, cls ? nH : nB, nN, mt, nt)) return false;
+    grp = uni(find_group(pre, g.G, mt));
+    local = cls ? -1 : mt - pre[grp];
+  } else {  // group by group
+    const int nM = g.tile_prefix[g.G];
+    if (!xcd_slot(blockIdx.x, nM * nN, id) || !tile_order(id, nM, nN, mt, nt)) return false;
+    grp = uni(find_group(g.tile_prefix, g.G, mt));
+    local = mt - g.tile_prefix[grp];
+  }
+  n0 = nt * BN;
+  const int rows = g.offsets[grp + 1] - g.offsets[grp];
+  local = local < 0 ? (rows / BM) * BM : local * BM;  // -1: the group's half tile
   row0 = uni(g.offsets[grp] + local);
-  mv = uni(min(BM, g.offsets[grp + 1] - g.offsets[grp] - local));
+  mv = uni(min(BM, rows - local));
   return mv > 0;
 }
 
@@ -151,7 +179,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
                                                        int E) {
   using C = typename Tilings<T>::Router;
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
-  RowGroups g{nullptr, nullptr, 1, Tn};
+  RowGroups g{nullptr, nullptr, nullptr, nullptr, 1, Tn, 0};
   int grp, row0, mv, n0;
   if (!resolve_rows(g, E, C::BM, C::BN, grp, row0, mv, n0)) return;
   OpDesc<T> a[1] = {{x + (int64_t)row0 * H, H, mv, H}};
@@ -344,7 +372,9 @@ __global__ __launch_bounds__(256) void k_hist(const int* __restrict__ idx, int T
 }
 
 // counts, exclusive offsets, per-block bases, and GEMM tile prefixes for the
-// row-tile heights in kTileBM.
+// row-tile heights in kTileBM: per height, the prefixes of all, big and half
+// row tiles (RowGroups), each [E + 1].
+constexpr int kTilePrefixes = 3;
 constexpr int kNumTileBM = 2;
 __constant__ int kTileBM[kNumTileBM] = {128, 256};
 
@@ -360,14 +390,20 @@ MOE_DEV int wave_incl_scan(int v) {
 }
 
 // With cnt[e] (LDS, e < E <= 1024) in place, a block of 1024 threads writes
-// the exclusive offsets (also to offs, LDS) and the tile prefix of every
+// the exclusive offsets (also to offs, LDS) and the tile prefixes of every
 // height in kTileBM, one expert per thread.  Integer arithmetic only.
 MOE_DEV void scan_counts(const int* cnt, int E, int* __restrict__ offsets,
                          int* __restrict__ tile_prefix, int* offs, int* wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int j = 0; j <= kNumTileBM; ++j) {
-    const int bm = j == 0 ? 1 : kTileBM[j - 1];
-    const int v = tid < E ? (cnt[tid] + bm - 1) / bm : 0;
+  for (int j = 0; j <= kTilePrefixes * kNumTileBM; ++j) {
+    const int c = tid < E ? cnt[tid] : 0;
+    int v = c;
+    if (j > 0) {
+      const int bm = kTileBM[(j - 1) / kTilePrefixes], r = c % bm, kind = (j - 1) % kTilePrefixes;
+      v = kind == 0 ? (c + bm - 1) / bm
+        : kind == 1 ? c / bm + (r > bm / 2 ? 1 : 0)
+                    : (r > 0 && r <= bm / 2 ? 1 : 0);
+    }
     const int incl = wave_incl_scan(v);
     if (lane == 63) wsum[wave] = incl;
     __syncthreads();
@@ -992,7 +1028,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
                                                       T* __restrict__ dx) {
   using C = typename Tilings<T>::Router;
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
-  RowGroups g{nullptr, nullptr, 1, Tn};
+  RowGroups g{nullptr, nullptr, nullptr, nullptr, 1, Tn, 0};
   int grp, row0, mv, n0;
   if (!resolve_rows(g, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   OpDesc<T> a[1] = {{dl + (int64_t)row0 * Epad, Epad, mv, Epad}};

@@ -188,7 +188,7 @@ struct moe_plan {
     fld(MOE_SAVED_PERM, 4 * TK);
     fld(MOE_SAVED_INV_PERM, 4 * TK);
     fld(MOE_SAVED_MEAN_PROB, 4 * (size_t)E);
-    L.tile_prefix = c.take(4 * (size_t)kNumTileBM * (E + 1));
+    L.tile_prefix = c.take(4 * (size_t)kTilePrefixes * kNumTileBM * (E + 1));
     const bool act = keep != Keep::Routing, pre = keep == Keep::All;
     fld(MOE_SAVED_X_PERM, act ? b * TK * H : 0);
     fld(MOE_SAVED_GATE_ACT, pre ? b * TK * I : 0);
@@ -519,7 +519,7 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
                          (const bf16_t*)sA, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else {
-    const RowGroups dense{nullptr, nullptr, 1, T};
+    const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
     hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
                        dim3(256), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, H, S, sG, sU, sA);
@@ -529,12 +529,22 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   }
 }
 
-// Calls f(tiling, row groups, row-tile upper bound) for a row-grouped launch
-// of tiling C: the tile-prefix table of C::BM and the grid bound TK/BM + E.
-template <class C, class F>
+// Calls f(tiling, row groups, grid(N)) for a row-grouped launch of tiling C
+// with N output columns: the tile prefixes of C::BM, and a grid
+// of the row-tile upper bound TK / BM + E times the column tiles, rounded up
+// to whole rounds of the 8 XCDs (xcd_slot2).  Half tiles run last when they
+// have a half-height tiling and the groups average at least two row tiles:
+// with fewer rows per expert (config 5: 256) the weight panels dominate the
+// traffic, and a half tile that runs apart from its expert's big tiles reads
+// them again (measured: config 2 gate/up forward 296 -> 249 us, config 5
+// row-grouped GEMMs 3-4 % slower).
+template <typename D, class C, class F>
 void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t TK, F&& f) {
-  f(C{}, RowGroups{offsets, tprefix_all + tile_slot(C::BM) * (E + 1), E, (int)TK},
-    ceil_div(TK, C::BM) + E);
+  const int* tp = tprefix_all + kTilePrefixes * tile_slot(C::BM) * (E + 1);
+  const int mt = ceil_div(TK, C::BM) + E;
+  const int half_last = has_half_rows<D, C>() && TK >= 2 * (int64_t)C::BM * E;
+  f(C{}, RowGroups{offsets, tp, tp + (E + 1), tp + 2 * (E + 1), E, (int)TK, half_last},
+    [mt](int N) { return 8 * ceil_div(mt * ceil_div(N, C::BN), 8); });
 }
 
 // The router GEMM has N = E: up to this many experts the 16 x 16 blocks of
@@ -584,9 +594,9 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
                            nullptr, (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G,
                            (bf16_t*)st.U, (bf16_t*)st.A);
     } else {
-      with_row_tiling<CG>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+      with_row_tiling<D, CG>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
         using C = decltype(c);
-        hipLaunchKernelGGL((k_gateup_fwd<D, true, C>), dim3(mt * ceil_div(I, C::BN)), dim3(256), 0,
+        hipLaunchKernelGGL((k_gateup_fwd<D, true, C>), dim3(grid(I)), dim3(256), 0,
                            s, st.xp, r, tg, nullptr, tu, nullptr, H, I, st.G, st.U, st.A);
       });
     }
@@ -603,9 +613,9 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
                            s, (const bf16_t*)st.A, nullptr, 1, 0, st.offsets, E, 0, (const bf16_t* const*)td,
                            nullptr, nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
     } else {
-      with_row_tiling<CB>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+      with_row_tiling<D, CB>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
         using C = decltype(c);
-        hipLaunchKernelGGL((k_down_fwd<D, true, C>), dim3(mt * ceil_div(H, C::BN)), dim3(256), 0, s,
+        hipLaunchKernelGGL((k_down_fwd<D, true, C>), dim3(grid(H)), dim3(256), 0, s,
                            st.A, r, td, nullptr, I, H, st.Y);
       });
     }
@@ -767,7 +777,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     D* sdU = (D*)(ws + W.sdU);
     dxs = (D*)(ws + W.dxs);
     const float sc = c.shared_expert_scale;
-    const RowGroups dense{nullptr, nullptr, 1, T};
+    const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
     hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
     launch_dense_wgrad<D, 1>(ss, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
@@ -802,9 +812,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_DOWN_DGRAD);
-    with_row_tiling<CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+    with_row_tiling<D, CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
-      hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(mt * ceil_div(I, C::BN)), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(grid(I)), dim3(256), 0, s,
                          dY, r, td, nullptr, H, I, 1.0f, G, U, dG, dU);
     });
     LAUNCH_CHECK();
@@ -822,9 +832,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_GATEUP_DGRAD);
-    with_row_tiling<CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, int mt) {
+    with_row_tiling<D, CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
-      hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(mt * ceil_div(H, C::BN)), dim3(256), 0,
+      hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(grid(H)), dim3(256), 0,
                          s, dG, dU, r, tg, nullptr, tu, nullptr, I, H, dXp);
     });
     LAUNCH_CHECK();

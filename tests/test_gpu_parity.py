@@ -132,6 +132,10 @@ BF16_CASES = [
     dict(T=384, H=128, E=64, k=6, I=64, S=128, skew=3.0),
     dict(T=256, H=256, E=256, k=8, I=128, S=128),
     dict(T=200, H=192, E=20, k=4, I=88, S=0, bias=True, norm_topk=True),
+    # >= 512 rows per expert: the row-grouped GEMMs run half-height tail tiles
+    # after every full tile (the tail order of configs 2 and 3)
+    dict(T=1300, H=128, E=4, k=3, I=96, S=32, bias=True),
+    dict(T=1100, H=136, E=4, k=2, I=200, S=0),
 ]
 
 
