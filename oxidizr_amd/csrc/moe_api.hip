@@ -150,6 +150,7 @@ struct moe_plan {
   // within each call, and fills the routed GEMMs' partial rounds of work.
   hipStream_t aux = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
+  hipEvent_t sdx = nullptr;  // backward: the shared expert's input gradient is ready
   // The backward's routed weight gradients and the router backward need only
   // dY / dG / dU and the routing state: they run on a third stream, beside
   // the input-gradient GEMMs of the call's stream.
@@ -757,8 +758,11 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   const KGroups kg{offsets, E, 0, 1, 0};
   float* partial = (float*)(ws + W.splitk_router);
   // Shared expert backward first, on the plan's second stream: it needs only
-  // d_out, x and its own saved activations; dx waits for it below.
+  // d_out, x and its own saved activations.  Its input gradient comes first
+  // (dx waits for that alone, event sdx), then its weight gradients, which
+  // like the routed ones on the third stream are joined only at the end.
   D* dxs = nullptr;
+  bool wait_sdx = false;
   SideJoin shared_join, wgrad_join;
   if (S > 0) {
     const hipStream_t ss = p->shared_stream(s);
@@ -780,10 +784,14 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
     hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
-    launch_dense_wgrad<D, 1>(ss, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
-                             partial_sh);
     hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0, ss, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, S, H, dxs);
+    if (ss != s) {
+      HIP_TRY(hipEventRecord(p->sdx, ss));
+      wait_sdx = true;
+    }
+    launch_dense_wgrad<D, 1>(ss, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
+                             partial_sh);
     launch_dense_wgrad<D, 2>(ss, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
                              (D*)g->shared_up, partial_sh);
     LAUNCH_CHECK();
@@ -862,8 +870,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     }
     LAUNCH_CHECK();
   }
-  HIP_TRY(wgrad_join.join());
-  HIP_TRY(shared_join.join());
+  // dx reads dXp and the router gradient (this stream) and the shared dx: the
+  // weight-gradient kernels still running on the side streams are joined after it
+  if (wait_sdx) HIP_TRY(hipStreamWaitEvent(s, p->sdx, 0));
   {
     StageTimer tm(p, s, MOE_STAGE_DX);
     hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, CR::BM) * ceil_div(H, CR::BN)),
@@ -872,6 +881,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     if (has_grad) hipLaunchKernelGGL(k_has_grad, dim3(ceil_div(E, 256)), dim3(256), 0, s, counts, E, has_grad);
     LAUNCH_CHECK();
   }
+  HIP_TRY(wgrad_join.join());
+  HIP_TRY(shared_join.join());
   return MOE_OK;
 }
 
@@ -965,6 +976,7 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
     e = hipStreamCreateWithFlags(&p->aux, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->join, hipEventDisableTiming);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&p->sdx, hipEventDisableTiming);
   }
   if (e == hipSuccess) e = hipStreamCreateWithFlags(&p->wgs, hipStreamNonBlocking);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wfork, hipEventDisableTiming);
@@ -991,6 +1003,7 @@ moe_status moe_plan_destroy(moe_plan* p) {
   if (p->aux) (void)hipStreamSynchronize(p->aux);
   if (p->fork) (void)hipEventDestroy(p->fork);
   if (p->join) (void)hipEventDestroy(p->join);
+  if (p->sdx) (void)hipEventDestroy(p->sdx);
   if (p->aux) (void)hipStreamDestroy(p->aux);
   if (p->wgs) (void)hipStreamSynchronize(p->wgs);
   for (hipEvent_t ev : {p->wfork, p->wmid, p->wjoin})
