@@ -134,8 +134,8 @@ BF16_CASES = [
     dict(T=200, H=192, E=20, k=4, I=88, S=0, bias=True, norm_topk=True),
     # >= 512 rows per expert: the row-grouped GEMMs run half-height tail tiles
     # after every full tile (the tail order of configs 2 and 3)
-    dict(T=1300, H=128, E=4, k=3, I=96, S=32, bias=True),
-    dict(T=1100, H=136, E=4, k=2, I=200, S=0),
+    dict(T=1300, H=128, E=4, k=3, I=96, S=32, bias=True, half_last=True),
+    dict(T=1280, H=136, E=4, k=2, I=200, S=0, half_last=True),
 ]
 
 
@@ -143,6 +143,7 @@ BF16_CASES = [
 def test_bf16_forward_backward_parity(spec):
     spec = dict(spec)
     skew = spec.pop("skew", None)
+    half_last = spec.pop("half_last", False)
     bias = None
     if skew is not None:
         bias = zipf_bias(spec["E"], s=1.2, beta=skew)
@@ -154,6 +155,11 @@ def test_bf16_forward_backward_parity(spec):
     _routing_equal(g, o)
     if skew is not None:
         assert (g["counts"] == 0).any(), "skewed case should leave some experts empty"
+    if half_last:  # the case must hold both kinds of last row tile (256-row tiles)
+        counts = np.asarray(g["counts"])
+        assert spec["T"] * spec["k"] >= 512 * spec["E"]
+        tails = counts % 256
+        assert ((tails > 0) & (tails <= 128)).any() and (tails > 128).any(), counts
     _check(case, g, o, 1e-2)
 
 
