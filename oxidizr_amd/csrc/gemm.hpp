@@ -663,6 +663,57 @@ MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, 
                                 [&](int m, int n, auto& v, const u32x4*) { f(m, n, v); });
 }
 
+// Row epilogue for bf16 outputs that need no element-wise work beyond a scale:
+// the accumulators of one 32-column block are scaled in fp32, rounded to bf16
+// (v_cvt_pk_bf16_f32, as store8 rounds) and staged through a wave-private LDS
+// region as packed pairs, half the LDS traffic of the fp32 staging above, then
+// read back as rows of 8 outputs: f(m_local, n_local, p) with p[x] the 16-byte
+// packed row of accumulator set x.  Row pitch 40 elements: the 8-byte writes
+// of 32 rows and the 16-byte reads of 4 rows per phase spread over the banks
+// (pitches 36 and 34 measured slower).  Same LDS preconditions as
+// for_each_row8.
+constexpr int kRowPitchBf16 = 40;
+template <class C, int NACC>
+constexpr int epi_lds_bf16_elems() { return 4 * NACC * C::WM * kRowPitchBf16; }
+template <class C, int NACC, class F>
+MOE_DEV void for_each_row8_bf16(const f32x16 (&acc)[NACC][C::TN][C::TM], bf16_t* lds, float scale,
+                                F&& f) {
+  static_assert(C::WM % 16 == 0, "rows are visited 16 at a time");
+  constexpr int P = kRowPitchBf16;
+  constexpr int RG = C::WM / 16;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wm = wave / C::WGN, wn = wave % C::WGN;
+  bf16_t* reg = lds + wave * NACC * C::WM * P;
+#pragma unroll
+  for (int tn = 0; tn < C::TN; ++tn) {  // unrolled: acc is indexed by constants only
+#pragma unroll
+    for (int x = 0; x < NACC; ++x)
+#pragma unroll
+      for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int row = tm * 32 + (lane & 31);
+          const int col = 8 * qq + 4 * (lane >> 5);
+          const f32x16& a = acc[x][tn][tm];
+          *reinterpret_cast<u32x2*>(reg + (x * C::WM + row) * P + col) =
+              u32x2{pack_bf16x2(scale * a[4 * qq], scale * a[4 * qq + 1]),
+                    pack_bf16x2(scale * a[4 * qq + 2], scale * a[4 * qq + 3])};
+        }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll 2
+    for (int g = 0; g < RG; ++g) {
+      const int row = g * 16 + (lane >> 2);
+      const int col = (lane & 3) * 8;
+      u32x4 pk[NACC];
+#pragma unroll
+      for (int x = 0; x < NACC; ++x)
+        pk[x] = *reinterpret_cast<const u32x4*>(reg + (x * C::WM + row) * P + col);
+      f(wm * C::WM + row, wn * C::WN + tn * 32 + col, pk);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // Store / load 8 consecutive elements (8-element aligned) of one row in global
 // memory.
 MOE_DEV void store8(bf16_t* p, const float* v) {

@@ -913,6 +913,20 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
   T* o0 = pick(out0_tab, out0_one, grp);
   T* o1 = NA == 2 ? pick(out1_tab, out1_one, grp) : nullptr;
   const int mv = min(C::BM, M - m0);
+  if constexpr (GROUPED && sizeof(T) == 2) {
+    // groups never split: alpha * acc rounded once, as store8 of the scaled
+    // value; the bf16 staging halves the epilogue's LDS traffic (the split
+    // branch below is compiled out, so the accumulators need no VGPR copy)
+    static_assert(epi_lds_bf16_elems<C, NA>() * 2 <= (int)sizeof(smem), "epilogue LDS");
+    for_each_row8_bf16<C, NA>(acc, reinterpret_cast<bf16_t*>(smem), alpha,
+                              [&](int m, int n, const u32x4 (&p)[NA]) {
+      if (m >= mv || n0 + n >= N) return;
+      const int64_t o = (int64_t)(m0 + m) * N + n0 + n;
+      *gptr(reinterpret_cast<u32x4*>(o0 + o)) = p[0];
+      if constexpr (NA == 2) *gptr(reinterpret_cast<u32x4*>(o1 + o)) = p[NA - 1];
+    });
+    return;
+  }
   static_assert(epi_lds_floats<C, NA>() * 4 <= (int)sizeof(smem), "epilogue LDS");
   if (groups.nsplit > 1) {  // fp32 partial tile of this chunk, [NA][nsplit][M][N]
     const int64_t MN = (int64_t)M * N;
