@@ -915,8 +915,9 @@ __global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T
   const int mv = min(C::BM, M - m0);
   if constexpr (GROUPED && sizeof(T) == 2) {
     // groups never split: alpha * acc rounded once, as store8 of the scaled
-    // value; the bf16 staging halves the epilogue's LDS traffic (the split
-    // branch below is compiled out, so the accumulators need no VGPR copy)
+    // value; the bf16 staging halves the epilogue's LDS traffic.  The packing
+    // copies the accumulators into VGPRs, which spilled while the split
+    // branch below shared the kernel; here that branch is compiled out.
     static_assert(epi_lds_bf16_elems<C, NA>() * 2 <= (int)sizeof(smem), "epilogue LDS");
     for_each_row8_bf16<C, NA>(acc, reinterpret_cast<bf16_t*>(smem), alpha,
                               [&](int m, int n, const u32x4 (&p)[NA]) {
