@@ -638,6 +638,42 @@ MOE_DEV void with_tile_rows(int mv, F&& body) {
   }
   body(C{});
 }
+// Likewise along N: a 256-column tile with at most 128 valid columns (the
+// last tile column when N % 256 is in 1..128, e.g. I = 1408) runs as a
+// 128-column tile with the four waves stacked along M (HalfCols<C>), with the
+// same per-element k order (same bits).  bf16 256-column tiles only.
+template <class C>
+using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, 1>;
+template <typename T, class C>
+constexpr bool has_half_cols() { return sizeof(T) == 2 && C::BN == 256; }
+template <typename T, class C, int NA, int NB, int NACC>
+constexpr int rowcol_smem_elems() {
+  constexpr int a = rowgroup_smem_elems<T, C, NA, NB, NACC>();
+  if constexpr (has_half_cols<T, C>()) {
+    constexpr int b = kernel_smem_elems<HalfCols<C>, T, NA, NB, NACC>();
+    return a > b ? a : b;
+  } else {
+    return a;
+  }
+}
+// body(tiling): half-height when at most BM / 2 rows are valid, else
+// half-width when at most BN / 2 of the nv remaining columns are valid.
+template <typename T, class C, class F>
+MOE_DEV void with_tile_shape(int mv, int nv, F&& body) {
+  if constexpr (has_half_rows<T, C>()) {
+    if (mv <= C::BM / 2) {
+      body(HalfRows<C>{});
+      return;
+    }
+  }
+  if constexpr (has_half_cols<T, C>()) {
+    if (nv <= C::BN / 2) {
+      body(HalfCols<C>{});
+      return;
+    }
+  }
+  body(C{});
+}
 
 template <typename T, bool GROUPED, class C = typename Tilings<T>::GateUp>
 __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
@@ -809,7 +845,7 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
                                                     const T* __restrict__ G,
                                                     const T* __restrict__ U,
                                                     T* __restrict__ dG, T* __restrict__ dU) {
-  __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
+  __shared__ __align__(16) T smem[rowcol_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);  // [H, N]: element (n, k=h) at wd + h*N + n
@@ -827,7 +863,7 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
       q[NV + j] = buf_ld16(ru, off + 16 * j, 0);
     }
   };
-  with_tile_rows<T, C>(mv, [&](auto ct) {
+  with_tile_shape<T, C>(mv, N - n0, [&](auto ct) {
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{dY + (int64_t)row0 * H, H, mv, H}};
     OpDesc<T> b[1] = {{wd + n0, N, N - n0, H}};
