@@ -136,6 +136,8 @@ BF16_CASES = [
     # after every full tile (the tail order of configs 2 and 3)
     dict(T=1300, H=128, E=4, k=3, I=96, S=32, bias=True, half_last=True),
     dict(T=1280, H=136, E=4, k=2, I=200, S=0, half_last=True),
+    # k above what dx prefetches per row group (bf16: 8)
+    dict(T=160, H=64, E=12, k=10, I=48, S=16),
 ]
 
 
