@@ -321,18 +321,33 @@ __global__ void k_colsum_final(const float* __restrict__ part, int nrb, int E, f
 }
 
 // aux = E (c_sw sum_e f_e P_e + c_sq sum_e P_e^2), z = mean_t lse_t^2.
+// counts == nullptr: the expert counts are built here from the top-k indices
+// (integer LDS histogram, E <= 1024), so the kernel can run beside the
+// dispatch instead of after it.
 __global__ __launch_bounds__(256) void k_losses(const float* __restrict__ P,
                                                 const int* __restrict__ counts,
+                                                const int* __restrict__ idx,
                                                 const float* __restrict__ lse, int Tn, int E,
                                                 int k, float c_sw, float c_sq,
                                                 float* __restrict__ aux, float* __restrict__ z) {
   __shared__ float r_sw[256], r_sq[256], r_z[256];
+  __shared__ int hist[1024];
   const int tid = threadIdx.x;
+  if (!counts) {
+    for (int e = tid; e < E; e += 256) hist[e] = 0;
+    __syncthreads();
+    const int64_t n = (int64_t)Tn * k;
+    for (int64_t i = tid; i < n; i += 256) {
+      const int e = idx[i];
+      if ((unsigned)e < (unsigned)E) atomicAdd(&hist[e], 1);
+    }
+    __syncthreads();
+  }
   const float inv_tk = 1.0f / ((float)Tn * (float)k);
   float sw = 0.0f, sq = 0.0f, zz = 0.0f;
   for (int e = tid; e < E; e += 256) {
     const float p = P[e];
-    sw += ((float)counts[e] * inv_tk) * p;
+    sw += ((float)(counts ? counts[e] : hist[e]) * inv_tk) * p;
     sq += p * p;
   }
   {

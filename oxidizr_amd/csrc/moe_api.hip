@@ -676,6 +676,16 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   }
   moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join);
   if (r != MOE_OK) return r;
+  {
+    // beside the dispatch when P is summed on the side stream (the kernel
+    // then counts the experts itself), else after the dispatch on s
+    const bool side = p_join.armed;
+    const hipStream_t ls = side ? p_join.side : s;
+    StageTimer tm(p, ls, MOE_STAGE_LOSSES);
+    hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, ls, st.P, side ? nullptr : st.counts,
+                       st.idx, st.lse, T, E, k, c.aux_switch_coef, c.aux_sqprob_coef, aux, z);
+    LAUNCH_CHECK();
+  }
   if ((r = routed_fwd<D>(p, s, T, x, st, true)) != MOE_OK) return r;
   HIP_TRY(shared_join.join());
   {
@@ -686,13 +696,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                        st.w, sY, c.shared_expert_scale, T, k, H, resid, out);
     LAUNCH_CHECK();
   }
-  HIP_TRY(p_join.join());  // P
-  {
-    StageTimer tm(p, s, MOE_STAGE_LOSSES);
-    hipLaunchKernelGGL(k_losses, dim3(1), dim3(256), 0, s, st.P, st.counts, st.lse, T, E, k,
-                       c.aux_switch_coef, c.aux_sqprob_coef, aux, z);
-    LAUNCH_CHECK();
-  }
+  HIP_TRY(p_join.join());  // P and the losses
   return MOE_OK;
 }
 
