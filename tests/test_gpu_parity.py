@@ -204,12 +204,15 @@ def test_bitwise_reproducible(dtype):
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
 
 
-@pytest.mark.parametrize("dtype,S", [("f32", 128), ("bf16", 128), ("bf16", 0)])
-def test_shared_stream_overlap_is_bitwise_serial(dtype, S):
+@pytest.mark.parametrize("dtype,S,E", [("f32", 128, 16), ("bf16", 128, 16), ("bf16", 0, 16),
+                                       ("bf16", 64, 2)])
+def test_shared_stream_overlap_is_bitwise_serial(dtype, S, E):
     # the shared expert on the plan's second stream and the weight gradients
-    # (and the forward's mean probabilities) on its third give the same bits
-    # as the serial order: no result depends on how the streams interleave
-    case = Case(T=640, H=128, E=16, k=2, I=64, S=S, dtype=dtype, w_std=0.05, seed=5)
+    # (and the forward's mean probabilities and losses) on its third give the
+    # same bits as the serial order: no result depends on how the streams
+    # interleave.  E = 2: 640 rows per expert, so the row-grouped GEMMs also
+    # run their half-height tiles last.
+    case = Case(T=640, H=128, E=E, k=2, I=64, S=S, dtype=dtype, w_std=0.05, seed=5)
     a = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=True)
     b = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=False)
     names = ["out", "aux", "z", "dx", "router", "gate", "up", "down"]
