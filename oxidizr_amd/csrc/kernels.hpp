@@ -124,12 +124,18 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
 // split into nsplit fixed chunks of kchunk rows (a multiple of the k-tile):
 // each chunk then produces an fp32 partial tile and k_splitk_reduce adds the
 // chunks in ascending order, so the result does not depend on scheduling.
+// col_walk: an XCD's tiles of a group run in tile_order (GM row tiles down a
+// column, then right) instead of row by row.  Measured on the weight
+// gradients: faster for the dense ones (shared expert: 1-3 %) and for groups
+// of >= 512 rows (configs 2 and 3: step -1.1 % / -0.4 %), slower for
+// config 5's ~256-row groups (gate/up pair +5 %).
 struct KGroups {
   const int* offsets;
   int G;
   int K;
   int nsplit;
   int kchunk;
+  int col_walk;
 };
 
 MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& split,
@@ -145,8 +151,15 @@ MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp,
   const int gs = uni(blockIdx.x / span);   // group (grouped) or split chunk (dense)
   int r;
   if (!xcd_slot(blockIdx.x - gs * span, per, r)) return false;
-  m0 = uni(r / nN) * BM;
-  n0 = uni(r % nN) * BN;
+  if (g.col_walk) {
+    int mt, nt;
+    if (!tile_order(r, nM, nN, mt, nt)) return false;
+    m0 = mt * BM;
+    n0 = nt * BN;
+  } else {
+    m0 = uni(r / nN) * BM;
+    n0 = uni(r % nN) * BN;
+  }
   if (g.offsets) {
     grp = gs;
     split = 0;

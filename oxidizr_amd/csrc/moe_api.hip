@@ -446,7 +446,7 @@ void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, co
   using C = typename std::conditional<NA == 2, typename Tilings<D>::WgradPair,
                                       typename Tilings<D>::Big>::type;
   const SplitPlan sp = plan_split<C>(M, N, T);
-  const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk};
+  const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk, 1};
   hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN)),
                      dim3(256), 0, s, P0, P1, ldp, Q,
                      ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
@@ -759,7 +759,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdg = (D* const*)(p->d_tab + 3 * E);
   D* const* tdu = (D* const*)(p->d_tab + 4 * E);
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
-  const KGroups kg{offsets, E, 0, 1, 0};
+  const KGroups kg{offsets, E, 0, 1, 0, TK >= 512 * (int64_t)E ? 1 : 0};
   float* partial = (float*)(ws + W.splitk_router);
   // Shared expert backward first, on the plan's second stream: it needs only
   // d_out, x and its own saved activations.  Its input gradient comes first
