@@ -67,9 +67,10 @@ MOE_DEV int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 // before moving one column right, so the ~32 workgroups resident on one XCD
 // cover about GM A panels and 32 / GM B panels, which its L2 holds, instead of
 // one A panel and 32 B panels.  Returns false for ids past the nM x nN tiles.
-// GM = 2 measured against 4 and 8: configs 3 and 5 0.6-0.9 % faster than with
-// 4 (their experts hold few row tiles, so pairs stay inside an expert more
-// often), config 2 unchanged; 8 was 1.5 % slower on config 5.
+// GM = 2 measured against 1, 3, 4 and 8: configs 3 and 5 0.6-0.9 % faster
+// than with 4 (their experts hold few row tiles, so pairs stay inside an
+// expert more often), config 2 unchanged; 1 was 1 % slower on configs 2 and 3,
+// 8 1.5 % slower on config 5, 3 within 0.3 % (run-to-run noise).
 MOE_DEV bool tile_order(int id, int nM, int nN, int& mt, int& nt) {
   constexpr int GM = 2;
   const int g = uni(id / (GM * nN));
