@@ -35,52 +35,6 @@ def gen_weights(torch, shape, std, gen, dtype, dev):
     return t
 
 
-def skew_bias(torch, wl, x, router, dev):
-    """Per-expert router logit bias that shapes the expert loads."""
-    import numpy as np
-    from oxidizr_amd.synth import lognormal_bias, zipf_bias
-    E, k = wl.E, wl.k
-    if wl.skew not in ("zipf", "lognormal"):
-        return None, {}
-    base = (x.float() @ router.float().t())
-    if wl.skew == "lognormal":
-        # target loads: lognormal(0, 0.5) shares of the T*k assignments; the
-        # per-expert logit bias is fitted to the realized top-k counts
-        target = np.exp(lognormal_bias(E, 0.5).astype(np.float64))
-        target = target / target.sum() * (wl.T * k)
-        tgt = torch.tensor(target, dtype=torch.float32, device=dev)
-        b = torch.log(tgt / tgt.mean()) * 0.1
-        for _ in range(60):
-            idx = torch.topk(base + b, k, dim=1).indices
-            c = torch.bincount(idx.flatten(), minlength=E).float()
-            b = b + 0.3 * torch.log((tgt + 1.0) / (c + 1.0))
-        idx = torch.topk(base + b, k, dim=1).indices
-        c = torch.bincount(idx.flatten(), minlength=E).float()
-        lc = torch.log(c.clamp(min=1.0))
-        return b, {"load_log_std": round(float(lc.std()), 3),
-                   "load_max_over_mean": round(float(c.max() / c.mean()), 2)}
-    mean = wl.T * k / E
-
-    def counts(beta):
-        b = torch.tensor(zipf_bias(E, 1.2, beta), device=dev)
-        idx = torch.topk(base + b, k, dim=1).indices
-        return torch.bincount(idx.flatten(), minlength=E), b
-
-    lo, hi = 0.0, 20.0
-    for _ in range(30):  # busiest expert at ~8x the mean load
-        mid = 0.5 * (lo + hi)
-        c, _ = counts(mid)
-        if c.max().item() < 8 * mean:
-            lo = mid
-        else:
-            hi = mid
-    c, b = counts(lo)
-    b = b.clone()
-    if (c == 0).sum().item() == 0:  # push the tail: the least likely expert gets no token
-        b[int(np.argmin(b.cpu().numpy()))] = -1e4
-    return b, {"zipf_beta": round(lo, 4)}
-
-
 def measured_traffic(workload):
     """Bytes per launch recorded in profiles/*.md ("traffic_bytes_per_launch
     <workload>: <bytes>"), or None."""
@@ -231,7 +185,7 @@ def main():
 
     import torch
     from oxidizr_amd.moe import MoeConfig, Plan
-    from oxidizr_amd.synth import WORKLOADS
+    from oxidizr_amd.synth import WORKLOADS, skew_bias
 
     wl = WORKLOADS[args.config]
     dev = torch.device("cuda:0")
@@ -250,7 +204,7 @@ def main():
         shared = (gen_weights(torch, (S, H), wl.w_std, gen, dtype, dev),
                   gen_weights(torch, (S, H), wl.w_std, gen, dtype, dev),
                   gen_weights(torch, (H, S), wl.w_std, gen, dtype, dev))
-    bias, skew_info = skew_bias(torch, wl, x, router, dev)
+    bias, skew_info = skew_bias(wl.T, wl.k, wl.E, wl.skew, x, router)
 
     cfg = MoeConfig(hidden_size=H, num_experts=E, experts_per_tok=k, intermediate_size=I,
                     shared_expert_enabled=S > 0, shared_intermediate_size=S or None,

@@ -90,6 +90,15 @@ typedef struct moe_plan moe_plan;
 moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** plan);
 moe_status moe_plan_destroy(moe_plan* plan);
 
+/* Whether a call over num_tokens tokens is supported by a plan of this
+ * configuration, without a device: MOE_OK, MOE_ERR_INVALID (bad config or
+ * negative count) or MOE_ERR_UNSUPPORTED (above 2^24 tokens, or an operand of
+ * num_tokens x max(H, I, S, E rounded up to 8) elements reaching 2^31 bytes:
+ * buffer loads take 32-bit offsets; split such a batch).  The forward and
+ * backward entry points make the same check.  No reference counterpart (the
+ * limit of this implementation; callers that batch tokens query it). */
+moe_status moe_check_tokens(const moe_config* cfg, int64_t num_tokens);
+
 /* Bytes of the caller-owned buffers for a call over num_tokens tokens. */
 size_t moe_saved_bytes(const moe_plan* plan, int64_t num_tokens);
 size_t moe_workspace_bytes(const moe_plan* plan, int64_t num_tokens);
@@ -135,7 +144,10 @@ moe_status moe_forward(moe_plan* plan, void* stream, int64_t num_tokens, const v
  * Writes dx [T, H] and every weight gradient (overwriting, not accumulating).
  * has_grad (device uint8 [E], may be NULL) receives 1 for experts that saw at
  * least one token; experts with has_grad 0 have no gradient entry
- * (src/trainer.rs:556-566) and their buffers are left untouched.
+ * (src/trainer.rs:556-566) and their buffers are left untouched.  With
+ * num_tokens = 0 has_grad and the dense gradients (router, router bias, shared
+ * expert) are set to zero.  Weight and gradient pointer tables are uploaded
+ * when they change, without synchronising the stream.
  * Replaces the boostr GradFn chain walked by backward_wrt (src/trainer.rs:1097). */
 moe_status moe_backward(moe_plan* plan, void* stream, int64_t num_tokens, const void* d_out,
                         const float* d_aux, const float* d_z, const void* x,

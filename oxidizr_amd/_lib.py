@@ -21,7 +21,7 @@ EXPORTED = [
     "moe_workspace_bytes", "moe_forward", "moe_backward", "moe_route_from_logits",
     "moe_saved_field_range", "moe_stage_name", "moe_plan_set_profiling", "moe_plan_stage_times",
     "moe_plan_set_shared_overlap", "moe_block_forward", "moe_block_backward",
-    "moe_last_error", "moe_version",
+    "moe_last_error", "moe_version", "moe_check_tokens",
 ]
 NUM_STAGES = 20
 
@@ -78,6 +78,8 @@ def load():
     L.moe_plan_create.restype = i32
     L.moe_plan_destroy.argtypes = [_vp]
     L.moe_plan_destroy.restype = i32
+    L.moe_check_tokens.argtypes = [P(MoeConfigC), i64]
+    L.moe_check_tokens.restype = i32
     L.moe_saved_bytes.argtypes = [_vp, i64]
     L.moe_saved_bytes.restype = sz
     L.moe_workspace_bytes.argtypes = [_vp, i64]

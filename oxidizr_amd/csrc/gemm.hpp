@@ -46,8 +46,13 @@ struct Tiling {
 // may also read neighbouring columns of the same matrix: their products only
 // reach output rows the epilogue drops).  For K-contiguous operands k_valid and
 // ld must be multiples of V; for transposed operands ld must be a multiple of V
-// and at least rows_valid rounded up to V.  Every byte the tile can reach lies
-// within 2^31 bytes of base (the host checks operand extents).
+// and at least rows_valid rounded up to V.  Every byte the tile can reach must
+// lie within 2^31 bytes of base: buffer offsets are 32-bit and kOobOffset
+// (2^31) must fall outside every resource.  Bases are the tile's own rows or
+// columns, so the extent is at most (rows or k of one group) x ld; the entry
+// points refuse token counts whose largest such extent (T x max(H, I, S, E)
+// elements, a group holding at most T rows) reaches 2^31 bytes
+// (moe_check_tokens), and plans whose weight matrices do.
 template <typename T>
 struct OpDesc {
   const T* base;

@@ -886,13 +886,16 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);  // [H, N]: element (n, k=h) at wd + h*N + n
   // G and U of a whole 32-column block are requested before its rows are
-  // visited; rows outside the tile read zeros (out-of-range offsets)
+  // visited; rows outside the tile read zeros (out-of-range offsets).  The
+  // resources start at the tile's first row and cover its mv rows, so the
+  // 32-bit offsets stay small whatever the number of routed rows.
   constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
-  const rsrc_t rg = make_rsrc(G, (uint32_t)((int64_t)groups.M * N * sizeof(T)));
-  const rsrc_t ru = make_rsrc(U, (uint32_t)((int64_t)groups.M * N * sizeof(T)));
+  const int64_t tile_base = (int64_t)row0 * N;
+  const rsrc_t rg = make_rsrc(G + tile_base, (uint32_t)((int64_t)mv * N * sizeof(T)));
+  const rsrc_t ru = make_rsrc(U + tile_base, (uint32_t)((int64_t)mv * N * sizeof(T)));
   auto pre = [&](int m, int n, u32x4 (&q)[2 * NV]) {
     const bool in = m < mv && n0 + n < N;
-    const uint32_t off = in ? (uint32_t)(((int64_t)(row0 + m) * N + n0 + n) * sizeof(T)) : kOobOffset;
+    const uint32_t off = in ? (uint32_t)(((int64_t)m * N + n0 + n) * sizeof(T)) : kOobOffset;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       q[j] = buf_ld16(rg, off + 16 * j, 0);
@@ -1171,6 +1174,20 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
 __global__ void k_has_grad(const int* __restrict__ counts, int E, uint8_t* __restrict__ has_grad) {
   const int e = blockIdx.x * blockDim.x + threadIdx.x;
   if (e < E) has_grad[e] = counts[e] > 0 ? 1 : 0;
+}
+
+// Sets n bytes at p to zero: 16-byte stores where p + i is 16-byte aligned
+// and whole, single bytes otherwise.  A kernel rather than hipMemsetAsync, so
+// a caller may capture the call in a HIP graph.
+__global__ __launch_bounds__(256) void k_zero(uint8_t* __restrict__ p, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * 256 + threadIdx.x) * 16;
+  if (i >= n) return;
+  if ((((uintptr_t)(p + i)) & 15u) == 0 && i + 16 <= n) {
+    *reinterpret_cast<u32x4*>(p + i) = u32x4{0u, 0u, 0u, 0u};
+    return;
+  }
+  const int64_t end = i + 16 < n ? i + 16 : n;
+  for (int64_t j = i; j < end; ++j) p[j] = 0;
 }
 
 // ------------------------------------------------------------------ fused RMSNorm (block path)

@@ -2,6 +2,7 @@
 // launch sequences.  Declared in include/moe_hip.h.
 #include <cstdarg>
 #include <cstdio>
+#include <algorithm>
 #include <cstring>
 #include <new>
 #include <string>
@@ -73,6 +74,9 @@ struct WsLayout {
 };
 
 int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
+// Buffer loads take 32-bit byte offsets and kOobOffset (2^31) must lie beyond
+// every resource: no operand extent may reach this many bytes.
+constexpr int64_t kMaxExtentBytes = int64_t(1) << 31;
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 int round8(int v) { return (v + 7) / 8 * 8; }
 
@@ -137,7 +141,14 @@ struct moe_plan {
   int device;
   // device pointer tables: 0 gate, 1 up, 2 down (weights); 3..5 their grads
   void** d_tab = nullptr;
-  void** h_tab = nullptr;       // pinned host staging
+  // Pinned host staging for table uploads: a ring of kTabSlots slots of 6 E
+  // pointers.  A slot is refilled only after the copy that last read it has
+  // run (its event), so an upload never waits for the stream as a whole.
+  static constexpr int kTabSlots = 16;
+  void** h_tab = nullptr;
+  hipEvent_t tab_ev[kTabSlots] = {};
+  bool tab_ev_pending[kTabSlots] = {};
+  int tab_next = 0;
   std::vector<const void*> cached[6];
   uint32_t profile_mask = 0;   // stages timed with HIP events (bit per moe_stage)
   struct Pending { int stage; hipEvent_t a, b; };
@@ -330,28 +341,50 @@ struct SideJoin {
 
 bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Copies the three host pointer tables tabs[0..2] into device tables
+// first..first + 2 when any of them changed since the last upload.  Every
+// pointer is checked before any state changes, so a refused call leaves the
+// cache and the device tables as they were.  The copy reads a pinned staging
+// slot of the ring; the host waits only for the copy that last used that slot
+// (kTabSlots uploads earlier), never for the stream.
 moe_status upload_tables(moe_plan* p, hipStream_t s, int first, const void* const* tabs[3]) {
   const int E = p->E();
   bool changed = false;
   for (int i = 0; i < 3; ++i) {
-    if (!tabs[i]) continue;
+    if (!tabs[i]) return fail(MOE_ERR_INVALID, "pointer table %d is NULL", first + i);
     auto& c = p->cached[first + i];
     if (c.size() != (size_t)E || memcmp(c.data(), tabs[i], sizeof(void*) * E) != 0) changed = true;
   }
   if (!changed) return MOE_OK;
-  // the staging buffer may still feed an earlier copy on this stream
-  HIP_TRY(hipStreamSynchronize(s));
-  for (int i = 0; i < 3; ++i) {
-    if (!tabs[i]) continue;
-    for (int e = 0; e < E; ++e) {
+  for (int i = 0; i < 3; ++i)
+    for (int e = 0; e < E; ++e)
       if (!tabs[i][e] || !aligned16(tabs[i][e]))
-        return fail(MOE_ERR_INVALID, "expert %d pointer %d is NULL or not 16-byte aligned", e, i);
-    }
-    memcpy(p->h_tab + (size_t)(first + i) * E, tabs[i], sizeof(void*) * E);
-    p->cached[first + i].assign(tabs[i], tabs[i] + E);
+        return fail(MOE_ERR_INVALID, "expert %d pointer %d is NULL or not 16-byte aligned", e,
+                    first + i);
+  const int slot = p->tab_next;
+  if (p->tab_ev_pending[slot]) {
+    HIP_TRY(hipEventSynchronize(p->tab_ev[slot]));
+    p->tab_ev_pending[slot] = false;
   }
-  HIP_TRY(hipMemcpyAsync(p->d_tab + (size_t)first * E, p->h_tab + (size_t)first * E,
-                         sizeof(void*) * 3 * E, hipMemcpyHostToDevice, s));
+  void** h = p->h_tab + (size_t)slot * 6 * E + (size_t)first * E;
+  for (int i = 0; i < 3; ++i) memcpy(h + (size_t)i * E, tabs[i], sizeof(void*) * E);
+  HIP_TRY(hipMemcpyAsync(p->d_tab + (size_t)first * E, h, sizeof(void*) * 3 * E,
+                         hipMemcpyHostToDevice, s));
+  HIP_TRY(hipEventRecord(p->tab_ev[slot], s));
+  p->tab_ev_pending[slot] = true;
+  p->tab_next = (slot + 1) % moe_plan::kTabSlots;
+  for (int i = 0; i < 3; ++i) p->cached[first + i].assign(tabs[i], tabs[i] + E);
+  return MOE_OK;
+}
+
+// Clears n bytes of device memory at q on stream s with a kernel (graph
+// capture records no memset node for it).
+moe_status zero_async(hipStream_t s, void* q, size_t n) {
+  if (!q || n == 0) return MOE_OK;
+  const int64_t vecs = ((int64_t)n + 15) / 16;
+  hipLaunchKernelGGL(k_zero, dim3((unsigned)((vecs + 255) / 256)), dim3(256), 0, s, (uint8_t*)q,
+                     (int64_t)n);
+  LAUNCH_CHECK();
   return MOE_OK;
 }
 
@@ -929,14 +962,39 @@ moe_status validate_config(const moe_config* c) {
     return fail(MOE_ERR_INVALID, "rms_norm_eps must be non-negative");
   if (c->fused_block && c->hidden > 8192)
     return fail(MOE_ERR_UNSUPPORTED, "fused_block supports hidden <= 8192 (got %d)", c->hidden);
+  // every weight matrix is read through one buffer resource (32-bit offsets)
+  const int64_t wide = std::max<int64_t>({c->intermediate, c->shared_intermediate,
+                                          round8(c->num_experts)});
+  if (wide * c->hidden * elt_size(c->dtype) >= kMaxExtentBytes)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "a weight matrix of %lld x %d elements reaches 2^31 bytes (32-bit buffer offsets)",
+                (long long)wide, c->hidden);
   return MOE_OK;
 }
 
-moe_status check_tokens(int64_t T) {
+// Largest buffer-resource extent of a call over T tokens, in bytes.  Operand
+// tiles start at their own rows, so an extent spans the rows (or, for a weight
+// gradient, the reduction rows) of one group: an expert holds at most T rows,
+// since a token picks k distinct experts.  The widest row is H, I, S or the
+// padded expert count of the router's logit gradient.
+int64_t max_token_extent(const moe_config& c, int64_t T) {
+  const int64_t wide = std::max<int64_t>({c.hidden, c.intermediate, c.shared_intermediate,
+                                          round8(c.num_experts)});
+  return T * wide * elt_size(c.dtype);
+}
+
+moe_status check_tokens_cfg(const moe_config& c, int64_t T) {
   if (T < 0) return fail(MOE_ERR_INVALID, "num_tokens (%lld) is negative", (long long)T);
   if (T > (1 << 24)) return fail(MOE_ERR_UNSUPPORTED, "num_tokens (%lld) above 2^24", (long long)T);
+  if (max_token_extent(c, T) >= kMaxExtentBytes)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "num_tokens (%lld): a %lld-byte operand reaches 2^31 bytes (32-bit buffer "
+                "offsets); split the batch",
+                (long long)T, (long long)max_token_extent(c, T));
   return MOE_OK;
 }
+
+moe_status check_tokens(const moe_plan* p, int64_t T) { return check_tokens_cfg(p->cfg, T); }
 
 }  // namespace
 
@@ -974,8 +1032,11 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
   p->device = device;
   const size_t tab_bytes = sizeof(void*) * 6 * (size_t)cfg->num_experts;
   hipError_t e = hipMalloc((void**)&p->d_tab, tab_bytes);
-  if (e == hipSuccess) e = hipHostMalloc((void**)&p->h_tab, tab_bytes, hipHostMallocDefault);
+  if (e == hipSuccess)
+    e = hipHostMalloc((void**)&p->h_tab, tab_bytes * moe_plan::kTabSlots, hipHostMallocDefault);
   if (e == hipSuccess) e = hipMemset(p->d_tab, 0, tab_bytes);
+  for (int i = 0; i < moe_plan::kTabSlots && e == hipSuccess; ++i)
+    e = hipEventCreateWithFlags(&p->tab_ev[i], hipEventDisableTiming);
   if (e == hipSuccess && cfg->shared_intermediate > 0) {
     e = hipStreamCreateWithFlags(&p->aux, hipStreamNonBlocking);
     if (e == hipSuccess) e = hipEventCreateWithFlags(&p->fork, hipEventDisableTiming);
@@ -1013,10 +1074,21 @@ moe_status moe_plan_destroy(moe_plan* p) {
   for (hipEvent_t ev : {p->wfork, p->wmid, p->wjoin})
     if (ev) (void)hipEventDestroy(ev);
   if (p->wgs) (void)hipStreamDestroy(p->wgs);
+  for (int i = 0; i < moe_plan::kTabSlots; ++i) {
+    if (!p->tab_ev[i]) continue;
+    if (p->tab_ev_pending[i]) (void)hipEventSynchronize(p->tab_ev[i]);
+    (void)hipEventDestroy(p->tab_ev[i]);
+  }
   if (p->d_tab) (void)hipFree(p->d_tab);
   if (p->h_tab) (void)hipHostFree(p->h_tab);
   delete p;
   return MOE_OK;
+}
+
+moe_status moe_check_tokens(const moe_config* cfg, int64_t T) {
+  moe_status st = validate_config(cfg);
+  if (st != MOE_OK) return st;
+  return check_tokens_cfg(*cfg, T);
 }
 
 size_t moe_saved_bytes(const moe_plan* p, int64_t T) {
@@ -1093,7 +1165,7 @@ moe_status forward_entry(moe_plan* p, void* stream, int64_t T, const void* x, co
                          void* saved, void* workspace, bool block) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
-  if ((st = check_tokens(T)) != MOE_OK) return st;
+  if ((st = check_tokens(p, T)) != MOE_OK) return st;
   if (!w) return fail(MOE_ERR_INVALID, "weights struct is NULL");
   const moe_config& c = p->cfg;
   if (block && !c.fused_block)
@@ -1114,9 +1186,8 @@ moe_status forward_entry(moe_plan* p, void* stream, int64_t T, const void* x, co
   hipStream_t s = (hipStream_t)stream;
   HIP_TRY(hipSetDevice(p->device));
   if (T == 0) {
-    if (aux_loss) HIP_TRY(hipMemsetAsync(aux_loss, 0, sizeof(float), s));
-    if (z_loss) HIP_TRY(hipMemsetAsync(z_loss, 0, sizeof(float), s));
-    return MOE_OK;
+    if ((st = zero_async(s, aux_loss, sizeof(float))) != MOE_OK) return st;
+    return zero_async(s, z_loss, sizeof(float));
   }
   const void* const* tabs[3] = {w->gate, w->up, w->down};
   if ((st = upload_tables(p, s, 0, tabs)) != MOE_OK) return st;
@@ -1151,7 +1222,7 @@ moe_status backward_entry(moe_plan* p, void* stream, int64_t T, const void* d_ou
                           void* dnw, const moe_grads* g, uint8_t* has_grad, bool block) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
-  if ((st = check_tokens(T)) != MOE_OK) return st;
+  if ((st = check_tokens(p, T)) != MOE_OK) return st;
   if (!w || !g) return fail(MOE_ERR_INVALID, "weights or grads struct is NULL");
   const moe_config& c = p->cfg;
   if (block && !c.fused_block)
@@ -1160,7 +1231,19 @@ moe_status backward_entry(moe_plan* p, void* stream, int64_t T, const void* d_ou
     return fail(MOE_ERR_INVALID, "the plan was created with fused_block = 1: call moe_block_backward");
   hipStream_t s = (hipStream_t)stream;
   HIP_TRY(hipSetDevice(p->device));
-  if (T == 0) return MOE_OK;  // nothing routed: no gradient is written
+  if (T == 0) {
+    // No token: no expert has a gradient entry (has_grad all 0, expert
+    // buffers untouched), and the dense gradients are sums over no token.
+    const size_t b = elt_size(c.dtype), H = c.hidden, E = c.num_experts,
+                 S = c.shared_intermediate;
+    const std::pair<void*, size_t> clear[] = {
+        {has_grad, E}, {g->router, E * H * b}, {g->router_bias, c.has_router_bias ? E * 4 : 0},
+        {g->shared_gate, S * H * b}, {g->shared_up, S * H * b}, {g->shared_down, H * S * b},
+        {block ? dnw : nullptr, H * b}};
+    for (const auto& q : clear)
+      if ((st = zero_async(s, q.first, q.second)) != MOE_OK) return st;
+    return MOE_OK;
+  }
   if (!d_out || !x || !saved || !workspace || !dx || !w->router || !w->gate || !w->up ||
       !w->down || !g->router || !g->gate || !g->up || !g->down || (block && (!nw || !dnw)))
     return fail(MOE_ERR_INVALID, "a required pointer is NULL");
@@ -1253,7 +1336,7 @@ moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const flo
                                  void* saved, void* workspace) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
-  if ((st = check_tokens(T)) != MOE_OK) return st;
+  if ((st = check_tokens(p, T)) != MOE_OK) return st;
   if (T == 0) return MOE_OK;
   if (!logits || !saved || !workspace) return fail(MOE_ERR_INVALID, "a required pointer is NULL");
   hipStream_t s = (hipStream_t)stream;

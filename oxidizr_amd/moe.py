@@ -96,6 +96,27 @@ def _p(t):
     return None if t is None else ctypes.c_void_p(t.data_ptr())
 
 
+# Scratch shared by every plan on a device: a call uses its workspace only
+# while its kernels run on the call's stream, so layers that run one after
+# another on one stream can share one buffer (sized for the largest call).
+# Keyed by (device, stream): calls on different streams may overlap and get
+# buffers of their own.
+_WORKSPACES = {}
+
+
+def shared_workspace(device, nbytes):
+    """A device buffer of at least nbytes shared per (device, current stream)."""
+    stream = torch.cuda.current_stream(device)
+    key = (str(device), stream.cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        # the old buffer may still be read by queued kernels: the caching
+        # allocator hands it out again only after this stream reaches here
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 class Plan:
     """A moe_plan bound to one device, plus reusable scratch buffers."""
 
@@ -120,9 +141,9 @@ class Plan:
         self.c = c
         h = ctypes.c_void_p()
         idx = self.device.index if self.device.index is not None else torch.cuda.current_device()
+        self.device = torch.device("cuda", idx)
         _lib.check(L.moe_plan_create(ctypes.byref(c), idx, ctypes.byref(h)))
         self.h = h
-        self._ws = {}
 
     def __del__(self):
         h = getattr(self, "h", None)
@@ -141,12 +162,11 @@ class Plan:
         return torch.empty(max(self.saved_bytes(T), 1), dtype=torch.uint8, device=self.device)
 
     def workspace(self, T):
-        n = max(self.workspace_bytes(T), 1)
-        ws = self._ws.get("buf")
-        if ws is None or ws.numel() < n:
-            ws = torch.empty(n, dtype=torch.uint8, device=self.device)
-            self._ws["buf"] = ws
-        return ws
+        return shared_workspace(self.device, self.workspace_bytes(T))
+
+    def check_tokens(self, T):
+        """Raises MoeError when a call over T tokens is not supported."""
+        _lib.check(_lib.load().moe_check_tokens(ctypes.byref(self.c), T))
 
     def saved_field(self, saved, T, name):
         """View of one field of a saved buffer as a typed tensor."""
@@ -293,6 +313,35 @@ class Plan:
         return {L.moe_stage_name(i).decode(): (ms[i], calls[i]) for i in range(_lib.NUM_STAGES)}
 
 
+class _RoutedExperts:
+    """Which experts received a token in a forward, copied to pinned host
+    memory right after the forward's dispatch (non-blocking). An expert with no
+    token gets no gradient entry (src/trainer.rs:556-566); by the time the
+    backward asks, the copy has long completed, so reading it does not stall
+    the launch pipeline the way a device-to-host copy in the backward would."""
+
+    def __init__(self, counts, num_experts):
+        self.num_experts = num_experts
+        if counts is None:  # no token: no expert is routed
+            self.host, self.event = None, None
+            return
+        self.host = torch.empty(counts.shape, dtype=counts.dtype, pin_memory=True)
+        self.host.copy_(counts, non_blocking=True)
+        self.event = torch.cuda.Event()
+        self.event.record()
+
+    def get(self):
+        if self.host is None:
+            return [False] * self.num_experts
+        self.event.synchronize()
+        return [c > 0 for c in self.host.tolist()]
+
+
+def _routed_experts_async(plan, saved, T):
+    E = plan.c.num_experts
+    return _RoutedExperts(plan.saved_field(saved, T, "counts") if T > 0 else None, E)
+
+
 class _MoeFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, layer, x2d, router, router_bias, *params):
@@ -305,6 +354,7 @@ class _MoeFunction(torch.autograd.Function):
         ctx.layer = layer
         ctx.plan = plan
         ctx.saved = saved
+        ctx.routed = _routed_experts_async(plan, saved, x2d.shape[0])
         ctx.save_for_backward(x2d, router, router_bias if router_bias is not None else x2d.new_empty(0),
                               *params)
         ctx.has_bias = router_bias is not None
@@ -327,12 +377,11 @@ class _MoeFunction(torch.autograd.Function):
         g_down = [torch.empty_like(t) for t in down]
         g_shared = [torch.empty_like(t) for t in shared] if shared is not None else None
         g, keep_g = plan.grads_struct(g_router, g_gate, g_up, g_down, g_bias, g_shared)
-        has_grad = torch.empty(E, dtype=torch.uint8, device=x2d.device)
         dout = dout.contiguous() if dout is not None else torch.zeros_like(x2d)
         daux = (daux if daux is not None else torch.zeros((), device=x2d.device)).float().contiguous()
         dz = (dz if dz is not None else torch.zeros((), device=x2d.device)).float().contiguous()
-        dx = plan.backward(x2d, dout, w, g, ctx.saved, d_aux=daux, d_z=dz, has_grad=has_grad)
-        hg = has_grad.cpu().tolist()  # host sync: which experts get a gradient entry
+        dx = plan.backward(x2d, dout, w, g, ctx.saved, d_aux=daux, d_z=dz)
+        hg = ctx.routed.get()  # experts that get a gradient entry, known since the forward
         ctx.saved = None
         def keep(lst):
             return [t if hg[e] else None for e, t in enumerate(lst)]
@@ -440,6 +489,7 @@ class _MoeBlockFunction(torch.autograd.Function):
         w, keep = plan.weights_struct(router, gate, up, down, router_bias, shared)
         out, aux, z, saved = plan.block_forward(h2d, norm_w, w)
         ctx.block, ctx.plan, ctx.saved = block, plan, saved
+        ctx.routed = _routed_experts_async(plan, saved, h2d.shape[0])
         ctx.has_bias = router_bias is not None
         ctx.save_for_backward(h2d, norm_w, router,
                               router_bias if router_bias is not None else h2d.new_empty(0), *params)
@@ -462,13 +512,11 @@ class _MoeBlockFunction(torch.autograd.Function):
         g_down = [torch.empty_like(t) for t in down]
         g_shared = [torch.empty_like(t) for t in shared] if shared is not None else None
         g, keep_g = plan.grads_struct(g_router, g_gate, g_up, g_down, g_bias, g_shared)
-        has_grad = torch.empty(E, dtype=torch.uint8, device=h2d.device)
         dout = dout.contiguous() if dout is not None else torch.zeros_like(h2d)
         daux = (daux if daux is not None else torch.zeros((), device=h2d.device)).float().contiguous()
         dz = (dz if dz is not None else torch.zeros((), device=h2d.device)).float().contiguous()
-        dh, d_norm_w = plan.block_backward(h2d, norm_w, dout, w, g, ctx.saved, d_aux=daux, d_z=dz,
-                                           has_grad=has_grad)
-        hg = has_grad.cpu().tolist()
+        dh, d_norm_w = plan.block_backward(h2d, norm_w, dout, w, g, ctx.saved, d_aux=daux, d_z=dz)
+        hg = ctx.routed.get()
         ctx.saved = None
 
         def keep(lst):

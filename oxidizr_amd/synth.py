@@ -123,3 +123,55 @@ def lognormal_bias(E, sigma=0.5, seed=0):
     """Per-expert logit bias log(load) with load ~ lognormal(0, sigma)."""
     rng = np.random.default_rng(seed + 54321)
     return rng.normal(0.0, sigma, size=E).astype(np.float32)
+
+
+def skew_bias(T, k, E, skew, x, router):
+    """Per-expert fp32 router-logit bias on the device that shapes the expert
+    loads of a BASELINE workload, and a dict describing the realised skew.
+
+    "zipf" (config 3): b_e = beta * log(rank_e^-1.2) over a seeded permutation,
+    beta bisected so the busiest expert gets about 8x the mean load; if no
+    expert is then empty, the least likely one is pushed to -1e4 (it gets no
+    token). "lognormal" (config 5): b_e fitted so the realised top-k loads
+    follow lognormal(0, 0.5) shares. "none": (None, {}).
+    x [T, H] and router [E, H] are device tensors; the bias depends on their
+    logits, so the same inputs always give the same bias."""
+    import torch
+    if skew not in ("zipf", "lognormal"):
+        return None, {}
+    dev = x.device
+    base = x.float() @ router.float().t()
+    if skew == "lognormal":
+        target = np.exp(lognormal_bias(E, 0.5).astype(np.float64))
+        target = target / target.sum() * (T * k)
+        tgt = torch.tensor(target, dtype=torch.float32, device=dev)
+        b = torch.log(tgt / tgt.mean()) * 0.1
+        for _ in range(60):
+            idx = torch.topk(base + b, k, dim=1).indices
+            c = torch.bincount(idx.flatten(), minlength=E).float()
+            b = b + 0.3 * torch.log((tgt + 1.0) / (c + 1.0))
+        idx = torch.topk(base + b, k, dim=1).indices
+        c = torch.bincount(idx.flatten(), minlength=E).float()
+        lc = torch.log(c.clamp(min=1.0))
+        return b, {"load_log_std": round(float(lc.std()), 3),
+                   "load_max_over_mean": round(float(c.max() / c.mean()), 2)}
+    mean = T * k / E
+
+    def counts(beta):
+        b = torch.tensor(zipf_bias(E, 1.2, beta), device=dev)
+        idx = torch.topk(base + b, k, dim=1).indices
+        return torch.bincount(idx.flatten(), minlength=E), b
+
+    lo, hi = 0.0, 20.0
+    for _ in range(30):  # busiest expert at ~8x the mean load
+        mid = 0.5 * (lo + hi)
+        c, _ = counts(mid)
+        if c.max().item() < 8 * mean:
+            lo = mid
+        else:
+            hi = mid
+    c, b = counts(lo)
+    b = b.clone()
+    if (c == 0).sum().item() == 0:  # push the tail: the least likely expert gets no token
+        b[int(np.argmin(b.cpu().numpy()))] = -1e4
+    return b, {"zipf_beta": round(lo, 4)}

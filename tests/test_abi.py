@@ -112,3 +112,42 @@ def test_required_moe_dims_messages():
     # shared_expert_enabled: None means true (src/config.rs:127-129)
     assert MoeConfig(64, 4, 2, 32).shared_width() == 32
     assert MoeConfig(64, 4, 2, 32, shared_expert_enabled=False).shared_width() == 0
+
+
+def test_c_caller_of_the_header(tmp_path):
+    # tests/c_abi_check.c: a plain C program compiled against include/moe_hip.h
+    # and linked with libmoe_hip.so, as a Rust FFI crate would bind it
+    _lib.load()
+    exe = tmp_path / "c_abi_check"
+    libdir = os.path.dirname(_lib.LIB_PATH)
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-I", os.path.join(ROOT, "include"),
+                    os.path.join(ROOT, "tests", "c_abi_check.c"), "-L", libdir, "-lmoe_hip",
+                    f"-Wl,-rpath,{libdir}", "-o", str(exe)], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True)
+    assert r.returncode == 0, r.stdout + r.stderr
+    assert "0 failure(s)" in r.stdout
+
+
+def _check_tokens(H, E, k, I, S, T, dtype=_lib.MOE_DTYPE_BF16):
+    L = _lib.load()
+    c = _lib.MoeConfigC()
+    L.moe_config_default(ctypes.byref(c), H, E, k, I, S)
+    c.dtype = dtype
+    return L.moe_check_tokens(ctypes.byref(c), T)
+
+
+def test_token_limit_follows_the_widest_operand():
+    # every operand tile is read through a buffer resource with 32-bit byte
+    # offsets: T * max(H, I, S, E rounded to 8) * bytes must stay below 2^31
+    for H, E, I, S in [(7168, 256, 2048, 2048), (2048, 64, 1408, 2816), (1024, 16, 4096, 0),
+                       (512, 1000, 256, 0)]:
+        for dt, b in ((_lib.MOE_DTYPE_BF16, 2), (_lib.MOE_DTYPE_F32, 4)):
+            wide = max(H, I, S, (E + 7) // 8 * 8)
+            limit = (2**31 - 1) // (wide * b)  # largest T with T * wide * b < 2^31
+            assert _check_tokens(H, E, 2, I, S, limit, dt) == 0, (H, E, I, S, dt)
+            if limit + 1 <= 2**24:
+                assert _check_tokens(H, E, 2, I, S, limit + 1, dt) == 4, (H, E, I, S, dt)
+    assert _check_tokens(32, 4, 2, 32, 0, 2**24) == 0     # 2^24 * 32 * 2 = 2^30 bytes
+    assert _check_tokens(32, 4, 2, 32, 0, 2**24 + 1) == 4  # above 2^24 tokens
+    assert _check_tokens(64, 4, 2, 32, 0, -1) == 1
+    assert _check_tokens(64, 4, 5, 32, 0, 8) == 1   # invalid config first

@@ -1,4 +1,4 @@
-"""GPU parity at BASELINE's full sizes (configs 2 and 4) against a plain
+"""GPU parity at BASELINE's full sizes (configs 2, 3, 4 and 5) against a plain
 PyTorch float32 reference of the same layer, on the same device tensors.
 
 The reference takes the layer's routing decision (top-k indices) from the HIP
@@ -7,16 +7,25 @@ recomputes everything else (logits, softmax, routing weights, expert SwiGLUs,
 shared expert, combine, aux loss) in float32 and differentiates it with torch
 autograd. The routing itself is checked bit-exactly against a top-k of the
 HIP path's own logits and through the dispatch invariants. Tolerance: the bf16
-bar, 1e-2 relative L2.
+bar, 1e-2 relative L2, per tensor (every expert projection is a tensor of its
+own in the reference, src/model.rs:1661-1672).
+
+Configs 3 and 5 run with their skewed routing (a per-expert router-logit bias:
+Zipf with an empty expert, lognormal loads up to ~4.6x the mean), so ragged
+and empty groups, full and partial row tiles and config 5's 112-deep k loops
+over 0.94 GB operands are all checked. Each full-size case also runs twice
+and must give the same bits.
 """
-import numpy as np
 import pytest
 import torch
 import torch.nn.functional as F
 
 from oxidizr_amd.moe import MoeConfig, Plan
+from oxidizr_amd.synth import skew_bias
 
 pytestmark = pytest.mark.gpu
+
+GRADS = ("router", "gate", "up", "down", "shared_gate", "shared_up", "shared_down")
 
 
 def rel(a, b):
@@ -28,7 +37,11 @@ def _problem(T, H, E, k, I, S, w_std, dev, seed=0):
     g = torch.Generator(device=dev)
     g.manual_seed(seed)
     bf = torch.bfloat16
-    n = lambda shape, std: (torch.randn(shape, generator=g, device=dev) * std).to(bf)
+
+    def n(shape, std):
+        t = torch.empty(shape, dtype=bf, device=dev)
+        return t.normal_(0.0, std, generator=g)
+
     p = {"x": n((T, H), 1.0), "dout": n((T, H), 1.0), "router": n((E, H), w_std),
          "gate": n((E, I, H), w_std), "up": n((E, I, H), w_std), "down": n((E, H, I), w_std)}
     if S:
@@ -37,29 +50,37 @@ def _problem(T, H, E, k, I, S, w_std, dev, seed=0):
     return p
 
 
-def _run(p, E, k, I, S, d_aux, backward=True):
+def _run(p, E, k, I, S, d_aux, backward=True, bias=None, fill=None):
+    """One forward (+ backward) through the C ABI. fill: value the expert
+    gradient buffers hold before the backward (untouched for has_grad 0)."""
     dev = p["x"].device
     T, H = p["x"].shape
     cfg = MoeConfig(hidden_size=H, num_experts=E, experts_per_tok=k, intermediate_size=I,
-                    shared_expert_enabled=S > 0, shared_intermediate_size=S or None)
+                    shared_expert_enabled=S > 0, shared_intermediate_size=S or None,
+                    router_bias=bias is not None)
     plan = Plan(cfg, torch.bfloat16, dev)
     shared = (p["shared_gate"], p["shared_up"], p["shared_down"]) if S else None
     w, _kw = plan.weights_struct(p["router"], list(p["gate"].unbind(0)), list(p["up"].unbind(0)),
-                                 list(p["down"].unbind(0)), None, shared)
+                                 list(p["down"].unbind(0)), bias, shared)
     out, aux, z, saved = plan.forward(p["x"], w)
     res = {"out": out, "aux": aux, "z": z}
     for f in ("logits", "topk_idx", "topk_w", "counts", "offsets", "perm", "inv_perm"):
         res[f] = plan.saved_field(saved, T, f)
     if backward:
         gr = {n: torch.empty_like(p[n]) for n in ("router", "gate", "up", "down")}
+        if fill is not None:
+            for n in ("gate", "up", "down"):
+                gr[n].fill_(fill)
+        gb = torch.empty_like(bias) if bias is not None else None
         gsh = [torch.empty_like(t) for t in shared] if S else None
         g, _kg = plan.grads_struct(gr["router"], list(gr["gate"].unbind(0)),
-                                   list(gr["up"].unbind(0)), list(gr["down"].unbind(0)), None, gsh)
-        has_grad = torch.empty(E, dtype=torch.uint8, device=dev)
+                                   list(gr["up"].unbind(0)), list(gr["down"].unbind(0)), gb, gsh)
+        has_grad = torch.full((E,), 7, dtype=torch.uint8, device=dev)
         res["dx"] = plan.backward(p["x"], p["dout"], w, g, saved,
                                   d_aux=torch.tensor(d_aux, device=dev),
                                   d_z=torch.tensor(0.0, device=dev), has_grad=has_grad)
         res.update(gr)
+        res["router_bias"] = gb
         res["has_grad"] = has_grad
         if S:
             res.update(shared_gate=gsh[0], shared_up=gsh[1], shared_down=gsh[2])
@@ -67,34 +88,55 @@ def _run(p, E, k, I, S, d_aux, backward=True):
     return res
 
 
-def _reference(p, idx, E, k, S, d_aux, backward=True):
-    """float32 layer on the given top-k indices, with torch autograd."""
-    t = {n: v.float().requires_grad_(backward and n != "dout") for n, v in p.items()}
-    x = t["x"]
+def _reference(p, idx, E, k, S, d_aux, backward=True, bias=None):
+    """float32 layer on the given top-k indices, differentiated by torch autograd.
+
+    Every expert projection is a leaf of its own (as in the reference), and the
+    expert outputs are built expert by expert over the tokens routed to each
+    (never a dense E x T product), so the restatement fits config 5. Returns
+    (out, aux, logits, grads) with grads[name] a tensor, or a list over experts
+    (None for an expert without tokens) for gate / up / down."""
+    req = backward
+    x = p["x"].float().requires_grad_(req)
+    router = p["router"].float().requires_grad_(req)
+    b = bias.float().clone().requires_grad_(req) if bias is not None else None
     T = x.shape[0]
-    logits = x @ t["router"].T
+    logits = x @ router.T
+    if b is not None:
+        logits = logits + b
     probs = torch.softmax(logits, dim=-1)
     wsel = probs.gather(1, idx.long())
-    out = torch.zeros_like(x)
     flat = idx.long().flatten()
+    order = torch.sort(flat, stable=True).indices  # expert ascending, then token ascending
+    counts = torch.bincount(flat, minlength=E)
+    offs = [0] + torch.cumsum(counts, 0).tolist()
+    leaves = [None] * E
+    ys = []
     for e in range(E):
-        sel = (flat == e).nonzero().flatten()
-        if sel.numel() == 0:
+        if offs[e + 1] == offs[e]:
             continue
-        tok = sel // k
-        xe = x.index_select(0, tok)
-        y = F.linear(F.silu(F.linear(xe, t["gate"][e])) * F.linear(xe, t["up"][e]), t["down"][e])
-        out = out.index_add(0, tok, wsel.flatten().index_select(0, sel)[:, None] * y)
+        wg, wu, wd = (p[n][e].float().requires_grad_(req) for n in ("gate", "up", "down"))
+        leaves[e] = (wg, wu, wd)
+        xe = x.index_select(0, order[offs[e]:offs[e + 1]] // k)
+        ys.append(F.linear(F.silu(F.linear(xe, wg)) * F.linear(xe, wu), wd))
+    Y = torch.cat(ys)
+    contrib = wsel.flatten().index_select(0, order)[:, None] * Y
+    out = torch.zeros_like(x).index_add(0, order // k, contrib)
+    sh = None
     if S:
-        out = out + F.linear(F.silu(F.linear(x, t["shared_gate"])) * F.linear(x, t["shared_up"]),
-                             t["shared_down"])
-    counts = torch.bincount(flat, minlength=E).float()
+        sh = [p[n].float().requires_grad_(req) for n in ("shared_gate", "shared_up", "shared_down")]
+        out = out + F.linear(F.silu(F.linear(x, sh[0])) * F.linear(x, sh[1]), sh[2])
     P = probs.mean(dim=0)
-    aux = E * ((counts / (T * k) * P).sum() + (P * P).sum())
+    aux = E * ((counts.float() / (T * k) * P).sum() + (P * P).sum())
     grads = None
     if backward:
-        ((out * t["dout"]).sum() + d_aux * aux).backward()
-        grads = {n: v.grad for n, v in t.items() if v.grad is not None}
+        ((out * p["dout"].float()).sum() + d_aux * aux).backward()
+        grads = {"x": x.grad, "router": router.grad,
+                 "router_bias": b.grad if b is not None else None}
+        for j, n in enumerate(("gate", "up", "down")):
+            grads[n] = [lv[j].grad if lv is not None else None for lv in leaves]
+        if S:
+            grads.update(shared_gate=sh[0].grad, shared_up=sh[1].grad, shared_down=sh[2].grad)
     return out.detach(), aux.detach(), logits.detach(), grads
 
 
@@ -110,10 +152,67 @@ def _check_routing(r, T, E, k):
     assert torch.equal(torch.sort(perm).values, torch.arange(T * k, device=perm.device))
     assert torch.equal(inv[perm], torch.arange(T * k, device=perm.device))
     # canonical order: expert ascending, then token ascending
-    assert torch.equal(idx.flatten()[perm], torch.repeat_interleave(torch.arange(E, device=perm.device), counts))
+    assert torch.equal(idx.flatten()[perm],
+                       torch.repeat_interleave(torch.arange(E, device=perm.device), counts))
     tok = perm // k
     same = idx.flatten()[perm][1:] == idx.flatten()[perm][:-1]
     assert bool((tok[1:] > tok[:-1])[same].all())
+
+
+def _check_grads(r, g, E, S, tol=1e-2, bias=False):
+    """Every gradient within tol (relative L2 per tensor: each expert's
+    projection on its own); experts without tokens keep their buffers."""
+    hg = r["has_grad"].bool()
+    counts = r["counts"]
+    assert torch.equal(hg, counts > 0)
+    errs = {"dx": rel(r["dx"].float(), g["x"]), "router": rel(r["router"].float(), g["router"])}
+    if bias:
+        errs["router_bias"] = rel(r["router_bias"], g["router_bias"])
+    for n in ("gate", "up", "down"):
+        worst, num, den = 0.0, 0.0, 0.0
+        for e in range(E):
+            if not bool(hg[e]):
+                assert g[n][e] is None
+                assert bool(torch.isnan(r[n][e]).all()), f"{n}[{e}] was written without a token"
+                continue
+            a, b = r[n][e].double(), g[n][e].double()
+            d2, b2 = float((a - b).pow(2).sum()), float(b.pow(2).sum())
+            worst = max(worst, (d2 / max(b2, 1e-60)) ** 0.5)
+            num, den = num + d2, den + b2
+        errs[n] = worst
+        errs[n + "_all"] = (num / den) ** 0.5
+    if S:
+        for n in ("shared_gate", "shared_up", "shared_down"):
+            errs[n] = rel(r[n].float(), g[n])
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"over {tol}: {bad} (all: {errs})"
+    return errs
+
+
+def _checksums(t):
+    """Two exact integer checksums of a bf16 / fp32 tensor's bits: the sum of
+    its 16-bit words, and their sum weighted by position mod 65521 (catches
+    moved values); equal bits give equal sums."""
+    w = t.contiguous().view(torch.int16).flatten().to(torch.int64)
+    pos = torch.arange(w.numel(), device=w.device, dtype=torch.int64) % 65521
+    return int(w.sum()), int((w * pos).sum())
+
+
+def _assert_rerun_bitwise(first, second, names):
+    for n in names:
+        if first.get(n) is None:
+            continue
+        if n in ("gate", "up", "down"):  # weight-sized: compared through checksums
+            assert first[n] == second[n], n
+        else:
+            assert torch.equal(first[n], second[n]), n
+
+
+def _digest(r):
+    d = dict(r)
+    for n in ("gate", "up", "down"):
+        d[n] = _checksums(torch.nan_to_num(r[n]))
+    return d
 
 
 def test_config2_full_size_forward_backward():
@@ -127,10 +226,58 @@ def test_config2_full_size_forward_backward():
     assert rel(r["out"].float(), out) < 1e-2
     assert abs(float(r["aux"]) - float(aux)) < 1e-3 * abs(float(aux))
     assert bool((r["has_grad"] == 1).all())
-    assert rel(r["dx"].float(), g["x"]) < 1e-2
-    assert rel(r["router"].float(), g["router"]) < 1e-2
-    for n in ("gate", "up", "down", "shared_gate", "shared_up", "shared_down"):
-        assert rel(r[n].float(), g[n]) < 1e-2, n
+    _check_grads(r, g, E, S)
+
+
+def test_config3_full_size_skewed_forward_backward():
+    # T=16384, E=64, top-6, two shared experts (S = 2 x 1408); Zipf(1.2) router
+    # bias: the busiest expert ~8x the mean load, at least one expert empty
+    dev = torch.device("cuda:0")
+    T, H, E, k, I, S = 16384, 2048, 64, 6, 1408, 2 * 1408
+    p = _problem(T, H, E, k, I, S, 0.02, dev, seed=3)
+    bias, _info = skew_bias(T, k, E, "zipf", p["x"], p["router"])
+    r = _run(p, E, k, I, S, d_aux=0.01, bias=bias, fill=float("nan"))
+    _check_routing(r, T, E, k)
+    counts = r["counts"]
+    assert int((counts == 0).sum()) >= 1
+    assert int(counts.max()) >= 6 * T * k // E  # busiest expert: several row tiles
+    assert torch.equal(r["has_grad"], (counts > 0).to(torch.uint8))
+    out, aux, logits, g = _reference(p, r["topk_idx"], E, k, S, d_aux=0.01, bias=bias)
+    assert rel(r["logits"], logits) < 1e-4
+    assert rel(r["out"].float(), out) < 1e-2
+    assert abs(float(r["aux"]) - float(aux)) < 1e-3 * abs(float(aux))
+    _check_grads(r, g, E, S, bias=True)
+    del g, out, logits
+    first = _digest(r)
+    again = _digest(_run(p, E, k, I, S, d_aux=0.01, bias=bias, fill=float("nan")))
+    _assert_rerun_bitwise(first, again, ("out", "aux", "z", "topk_idx", "perm", "dx", "router",
+                                         "router_bias", "has_grad") + GRADS)
+
+
+def test_config5_full_size_skewed_forward_backward():
+    # DeepSeek-V3-like width: T=8192, H=7168, E=256, top-8, I=2048, shared 2048,
+    # weights N(0, 0.006), lognormal(0.5) expert loads (full and partial 256-row
+    # tiles, experts up to ~1170 rows, 112 k-tiles over H)
+    dev = torch.device("cuda:0")
+    T, H, E, k, I, S = 8192, 7168, 256, 8, 2048, 2048
+    p = _problem(T, H, E, k, I, S, 0.006, dev, seed=5)
+    bias, _info = skew_bias(T, k, E, "lognormal", p["x"], p["router"])
+    r = _run(p, E, k, I, S, d_aux=0.01, bias=bias, fill=float("nan"))
+    _check_routing(r, T, E, k)
+    counts = r["counts"]
+    assert int(counts.max()) > 2 * 256  # an expert spanning several row tiles
+    assert int(((counts % 256) > 0).sum()) > E // 2  # many partial last tiles
+    out, aux, logits, g = _reference(p, r["topk_idx"], E, k, S, d_aux=0.01, bias=bias)
+    assert rel(r["logits"], logits) < 1e-4
+    assert rel(r["out"].float(), out) < 1e-2
+    assert abs(float(r["aux"]) - float(aux)) < 1e-3 * abs(float(aux))
+    _check_grads(r, g, E, S, bias=True)
+    del g, out, logits
+    first = _digest(r)
+    del r
+    again = _digest(_run(p, E, k, I, S, d_aux=0.01, bias=bias, fill=float("nan")))
+    _assert_rerun_bitwise(first, again, ("out", "aux", "z", "topk_idx", "perm", "dx", "router",
+                                         "router_bias", "has_grad") + GRADS)
 
 
 def test_config4_full_size_forward():
@@ -148,10 +295,33 @@ def test_config4_full_size_forward():
 
 def test_empty_batch_and_single_expert():
     dev = torch.device("cuda:0")
-    # T = 0: aux and z are 0, nothing is launched
-    p = _problem(0, 64, 4, 2, 32, 0, 0.05, dev)
-    r = _run(p, 4, 2, 32, 0, d_aux=0.0)
-    assert r["out"].shape == (0, 64) and float(r["aux"]) == 0.0 and float(r["z"]) == 0.0
+    # T = 0: aux and z are 0; the backward sets has_grad and the dense
+    # gradients (router, router bias, shared expert) to zero and leaves the
+    # expert buffers untouched
+    p = _problem(0, 64, 4, 2, 32, 32, 0.05, dev)
+    bias = torch.zeros(4, device=dev)
+    cfg = MoeConfig(hidden_size=64, num_experts=4, experts_per_tok=2, intermediate_size=32,
+                    shared_intermediate_size=32, router_bias=True)
+    plan = Plan(cfg, torch.bfloat16, dev)
+    shared = (p["shared_gate"], p["shared_up"], p["shared_down"])
+    w, _kw = plan.weights_struct(p["router"], list(p["gate"].unbind(0)), list(p["up"].unbind(0)),
+                                 list(p["down"].unbind(0)), bias, shared)
+    out, aux, z, saved = plan.forward(p["x"], w)
+    gr = {n: torch.full_like(p[n], float("nan")) for n in ("router", "gate", "up", "down")}
+    gb = torch.full_like(bias, float("nan"))
+    gsh = [torch.full_like(t, float("nan")) for t in shared]
+    g, _kg = plan.grads_struct(gr["router"], list(gr["gate"].unbind(0)), list(gr["up"].unbind(0)),
+                               list(gr["down"].unbind(0)), gb, gsh)
+    has_grad = torch.full((4,), 7, dtype=torch.uint8, device=dev)
+    plan.backward(p["x"], p["dout"], w, g, saved, d_aux=torch.tensor(0.01, device=dev),
+                  has_grad=has_grad)
+    torch.cuda.synchronize()
+    assert out.shape == (0, 64) and float(aux) == 0.0 and float(z) == 0.0
+    assert bool((has_grad == 0).all())
+    assert bool((gr["router"] == 0).all()) and bool((gb == 0).all())
+    assert all(bool((t == 0).all()) for t in gsh)
+    for n in ("gate", "up", "down"):
+        assert bool(torch.isnan(gr[n]).all()), n
     # E = k = 1: the layer is one dense SwiGLU with routing weight 1
     p = _problem(40, 64, 1, 1, 32, 0, 0.05, dev, seed=2)
     r = _run(p, 1, 1, 32, 0, d_aux=0.0)

@@ -9,11 +9,14 @@ The oracle routes from the GPU's own logits (logits_in), so both sides take
 the same routing decisions; the GPU logits themselves are compared with
 tolerance.
 """
+import ctypes
+
 import numpy as np
 import pytest
 import torch
 
 from oracle import moe_oracle as mo
+from oxidizr_amd import _lib
 from oxidizr_amd.moe import MoeConfig, MoeLayer, Plan
 from oxidizr_amd.synth import zipf_bias
 from tests.gpu_helpers import Case, gpu_block_run, gpu_run, oracle_run, rel, rounded
@@ -289,6 +292,11 @@ def test_recompute_activations_is_bitwise_equal(dtype, T):
     for n in ("out", "aux", "z", "dx", "router", "gate", "up", "down", "shared_gate",
               "shared_up", "shared_down", "has_grad", "topk_idx", "perm"):
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+    # and the recomputing path against the oracle itself (the reference keeps
+    # the recomputed layer numerically right: src/model/recompute/segment.rs:337-362)
+    o = oracle_run(rec, b["logits"], d_aux=0.01, d_z=0.001)
+    _routing_equal(b, o)
+    _check(rec, b, o, 1e-5 if dtype == "f32" else 1e-2)
 
 
 def test_recompute_shrinks_saved_state():
@@ -351,6 +359,24 @@ def test_block_recompute_is_bitwise_equal(dtype):
     for n in ("out", "aux", "z", "dh", "norm_weight", "router", "gate", "up", "down",
               "shared_gate", "shared_up", "shared_down"):
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+    # the recomputed block against the block oracle
+    p = case.p
+    o = mo.MoeBlockOracle(case.ocfg, 1e-6)
+    out, aux, z = o.forward(h, nw, p["router"], p["gate"], p["up"], p["down"], None,
+                            p["shared_gate"], p["shared_up"], p["shared_down"],
+                            logits_in=b["logits"])
+    og = o.backward(p["dout"], d_aux=0.01, d_z=0.0)
+    tol = 1e-5 if dtype == "f32" else 1e-2
+    hg = og["has_grad"].astype(bool)
+    errs = {"out": rel(b["out"], out), "dh": rel(b["dh"], og["h"]),
+            "d_norm_weight": rel(b["norm_weight"], og["norm_weight"]),
+            "d_router": rel(b["router"], og["router"])}
+    for n in ("gate", "up", "down"):
+        errs["d_" + n] = rel(b[n][hg], og[n][hg])
+    for n in ("shared_gate", "shared_up", "shared_down"):
+        errs["d_" + n] = rel(b[n], og[n])
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"over tolerance {tol}: {bad} (all: {errs})"
 
 
 def test_block_plan_rejects_plain_entry_points():
@@ -386,8 +412,180 @@ def test_layer_from_packed_checkpoint_matches(tmp_path):
     plan = Plan(case.cfg, torch.bfloat16, dev)
     w, _keep = pk.weights_struct(plan)
     x = torch.tensor(p["x"], device=dev).to(torch.bfloat16)
-    out, aux, z, _ = plan.forward(x, w)
+    dout = torch.tensor(p["dout"], device=dev).to(torch.bfloat16)
+    out, aux, z, saved = plan.forward(x, w)
+    # gradients into packed [E, I, H] / [E, H, I] storage as well
+    gpk = PackedExperts.empty(128, 8, 64, 64, dtype=torch.bfloat16, device=dev)
+    for t in (gpk.gate, gpk.up, gpk.down):
+        t.fill_(float("nan"))
+    g, _keep_g = gpk.grads_struct(plan)
+    has_grad = torch.empty(8, dtype=torch.uint8, device=dev)
+    dx = plan.backward(x, dout, w, g, saved, d_aux=torch.tensor(0.01, device=dev),
+                       d_z=torch.tensor(0.0, device=dev), has_grad=has_grad)
     torch.cuda.synchronize()
-    ref = gpu_run(case, backward=False)
-    np.testing.assert_array_equal(out.float().cpu().numpy(), ref["out"])
+    logits = plan.saved_field(saved, 200, "logits").cpu().numpy()
+    o = oracle_run(case, logits, d_aux=0.01)
+    got = {"out": out.float().cpu().numpy(), "aux": aux.cpu().numpy(), "z": z.cpu().numpy(),
+           "logits": logits, "has_grad": has_grad.cpu().numpy(), "dx": dx.float().cpu().numpy()}
+    for f in ("probs", "topk_w", "topk_idx", "counts", "offsets", "perm", "inv_perm"):
+        got[f] = plan.saved_field(saved, 200, f).cpu().numpy()
+    for n in ("router", "gate", "up", "down"):
+        got[n] = getattr(gpk, n).float().cpu().numpy()
+    got["shared_gate"], got["shared_up"], got["shared_down"] = (
+        t.float().cpu().numpy() for t in gpk.shared)
+    _routing_equal(got, o)
+    _check(case, got, o, 1e-2)
+    # and the same bits as the same weights held as separate tensors
+    ref = gpu_run(case, d_aux=0.01)
+    np.testing.assert_array_equal(got["out"], ref["out"])
+    np.testing.assert_array_equal(got["dx"], ref["dx"])
     assert float(aux) == float(ref["aux"])
+
+
+# ---------------------------------------------------------------- the drop-in module
+
+def _layer_from_case(case, dev):
+    layer = MoeLayer(case.cfg, dtype=case.tdtype, device=dev)
+    p = case.p
+    with torch.no_grad():
+        layer.router.gate.weight.copy_(torch.tensor(p["router"]))
+        for e, ex in enumerate(layer.experts):
+            ex.gate_proj.weight.copy_(torch.tensor(p["gate"][e]))
+            ex.up_proj.weight.copy_(torch.tensor(p["up"][e]))
+            ex.down_proj.weight.copy_(torch.tensor(p["down"][e]))
+        if case.S:
+            for n in ("gate", "up", "down"):
+                getattr(layer.shared_expert, f"{n}_proj").weight.copy_(
+                    torch.tensor(p[f"shared_{n}"]))
+        if case.bias is not None:
+            layer.router.bias.copy_(torch.tensor(p["router_bias"]))
+    return layer
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_moe_layer_autograd_backward_matches_oracle(dtype):
+    # MoeLayer(x [B, S, H]) -> (out, aux, z), then loss.backward() through the
+    # autograd node: the Python stand-in of the Rust GradFn. Gradients land in
+    # .grad in the reference's parameter order; an expert without a token gets
+    # no gradient entry (.grad stays None, src/trainer.rs:556-566).
+    bias = np.array([0, 0, -1e4, 0, 0, 0, 0, -1e4], np.float32)  # experts 2, 7 never chosen
+    case = Case(T=120, H=64, E=8, k=2, I=48, S=32, dtype=dtype, w_std=0.1, seed=41, bias=bias)
+    dev = torch.device("cuda:0")
+    layer = _layer_from_case(case, dev)
+    # parameter identity and order (src/model.rs:1887-1897, names :4890-4910)
+    names = [n for n, _ in layer.trainable_parameters()]
+    want = ["router.gate.weight", "router.gate.bias"]
+    for e in range(8):
+        want += [f"experts.{e}.{n}_proj.weight" for n in ("gate", "up", "down")]
+    want += [f"shared_expert.{n}_proj.weight" for n in ("gate", "up", "down")]
+    assert names == want
+    assert all(a is b for (_, a), b in zip(layer.trainable_parameters(),
+                                          [layer.router.gate.weight, layer.router.bias] +
+                                          [getattr(ex, f"{n}_proj").weight
+                                           for ex in layer.experts for n in ("gate", "up", "down")] +
+                                          [getattr(layer.shared_expert, f"{n}_proj").weight
+                                           for n in ("gate", "up", "down")]))
+    x = torch.tensor(case.p["x"], device=dev).to(case.tdtype).reshape(2, 60, 64).requires_grad_()
+    dout = torch.tensor(case.p["dout"], device=dev).to(case.tdtype).reshape(2, 60, 64)
+    out, aux, z = layer(x)
+    assert out.shape == (2, 60, 64)
+    ((out * dout).sum() + 0.01 * aux + 0.001 * z).backward()
+    torch.cuda.synchronize()
+    logits = gpu_run(case, backward=False)["logits"]
+    o = oracle_run(case, logits, d_aux=0.01, d_z=0.001)
+    tol = 1e-5 if dtype == "f32" else 1e-2
+    errs = {"out": rel(out.detach().float().cpu().numpy().reshape(120, 64), o["out"]),
+            "aux": abs(float(aux) - o["aux"]) / abs(o["aux"]),
+            "z": abs(float(z) - o["z"]) / abs(o["z"]),
+            "dx": rel(x.grad.float().cpu().numpy().reshape(120, 64), o["x"]),
+            "router": rel(layer.router.gate.weight.grad.float().cpu().numpy(), o["router"]),
+            "router_bias": rel(layer.router.bias.grad.float().cpu().numpy(), o["router_bias"])}
+    for e, ex in enumerate(layer.experts):
+        for n in ("gate", "up", "down"):
+            grad = getattr(ex, f"{n}_proj").weight.grad
+            if not o["has_grad"][e]:
+                assert grad is None, (e, n)
+                continue
+            errs[f"{n}{e}"] = rel(grad.float().cpu().numpy(), o[n][e])
+    for n in ("gate", "up", "down"):
+        errs[f"shared_{n}"] = rel(getattr(layer.shared_expert, f"{n}_proj").weight.grad.float()
+                                  .cpu().numpy(), o[f"shared_{n}"])
+    assert list(o["has_grad"]) == [1, 1, 0, 1, 1, 1, 1, 0]
+    bad = {n: e for n, e in errs.items() if not e <= tol}
+    assert not bad, f"over tolerance {tol}: {bad} (all: {errs})"
+
+
+def test_alternating_gradient_buffers_match_oracle():
+    # Three backward calls into two alternating sets of gradient buffers (the
+    # pointer tables change on every call; they are uploaded through the
+    # plan's staging ring, without synchronising the stream): every call's
+    # gradients must match the oracle.
+    case = Case(T=150, H=64, E=8, k=2, I=48, S=32, dtype="bf16", w_std=0.1, seed=43)
+    dev = torch.device("cuda:0")
+    t = {n: torch.tensor(v, device=dev).to(torch.bfloat16) for n, v in case.p.items()}
+    plan = Plan(case.cfg, torch.bfloat16, dev)
+    gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
+    shared = (t["shared_gate"], t["shared_up"], t["shared_down"])
+    w, _kw = plan.weights_struct(t["router"], gate, up, down, None, shared)
+    out, aux, z, saved = plan.forward(t["x"], w)
+    sets = []
+    for _ in range(2):
+        gr = {n: torch.full_like(t[n], float("nan")) for n in ("router", "gate", "up", "down")}
+        gsh = [torch.full_like(a, float("nan")) for a in shared]
+        g, keep = plan.grads_struct(gr["router"], list(gr["gate"].unbind(0)),
+                                    list(gr["up"].unbind(0)), list(gr["down"].unbind(0)), None, gsh)
+        sets.append((gr, gsh, g, keep))
+    dxs = []
+    for call in range(3):
+        gr, gsh, g, _keep = sets[call % 2]
+        dxs.append(plan.backward(t["x"], t["dout"], w, g, saved,
+                                 d_aux=torch.tensor(0.01, device=dev)).float().cpu().numpy())
+        torch.cuda.synchronize()
+        got = {"dx": dxs[-1], "router": gr["router"].float().cpu().numpy()}
+        for n in ("gate", "up", "down"):
+            got[n] = gr[n].float().cpu().numpy()
+        for n, a in zip(("shared_gate", "shared_up", "shared_down"), gsh):
+            got[n] = a.float().cpu().numpy()
+        if call == 0:
+            logits = plan.saved_field(saved, 150, "logits").cpu().numpy()
+            o = oracle_run(case, logits, d_aux=0.01)
+        hg = o["has_grad"].astype(bool)
+        errs = {"dx": rel(got["dx"], o["x"]), "router": rel(got["router"], o["router"])}
+        for n in ("gate", "up", "down"):
+            errs[n] = rel(got[n][hg], o[n][hg])
+            assert np.isnan(got[n][~hg]).all(), (call, n)
+        for n in ("shared_gate", "shared_up", "shared_down"):
+            errs[n] = rel(got[n], o[n])
+        assert max(errs.values()) <= 1e-2, (call, errs)
+        for gt in (gr["router"], gr["gate"], gr["up"], gr["down"], *gsh):
+            gt.fill_(float("nan"))  # the next call into this set must rewrite it
+    np.testing.assert_array_equal(dxs[0], dxs[2])
+
+
+def test_refused_table_leaves_the_plan_usable():
+    # A call refused for a bad expert pointer must not leave the plan's cached
+    # tables half-updated: the next good call with changed tables uploads them.
+    case = Case(T=64, H=64, E=4, k=2, I=32, S=0, dtype="f32", w_std=0.1, seed=45)
+    dev = torch.device("cuda:0")
+    t = {n: torch.tensor(v, device=dev) for n, v in case.p.items()}
+    plan = Plan(case.cfg, torch.float32, dev)
+    gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
+    w, _k = plan.weights_struct(t["router"], gate, up, down)
+    first, _a, _b, _s = plan.forward(t["x"], w, need_grad=False)
+    gate2 = [g.clone() * 2.0 for g in gate]
+    bad = _lib.MoeWeightsC()
+    bad.router = t["router"].data_ptr()
+    tabs = [_lib.ptr_array([a.data_ptr() for a in gate2]),
+            _lib.ptr_array([a.data_ptr() for a in up]),
+            _lib.ptr_array([a.data_ptr() for a in down[:-1]] + [0])]  # NULL down pointer
+    bad.gate, bad.up, bad.down = (ctypes.cast(a, ctypes.c_void_p) for a in tabs)
+    with pytest.raises(_lib.MoeError, match="NULL"):
+        plan.forward(t["x"], bad, need_grad=False)
+    w2, _k2 = plan.weights_struct(t["router"], gate2, up, down)
+    second, _a, _b, _s = plan.forward(t["x"], w2, need_grad=False)
+    torch.cuda.synchronize()
+    case2 = Case(T=64, H=64, E=4, k=2, I=32, S=0, dtype="f32", w_std=0.1, seed=45)
+    case2.p["gate"] = case.p["gate"] * 2.0
+    g2 = gpu_run(case2, backward=False)
+    np.testing.assert_array_equal(second.cpu().numpy(), g2["out"])
+    assert not np.array_equal(first.cpu().numpy(), second.cpu().numpy())
