@@ -25,9 +25,10 @@ namespace moe {
 
 // BM x BN output tile per workgroup of 4 waves arranged WGM x WGN (wave w
 // owns block (w / WGN, w % WGN)), BK-deep k-tiles.
-template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2>
+template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2, int NST_ = 2>
 struct Tiling {
   static constexpr int BM = BM_, BN = BN_, BK = BK_;
+  static constexpr int NST = NST_;        // LDS pipeline stages (direct-to-LDS loop)
   static constexpr int V = Vec16<T>::N;   // elements per 16-byte vector
   static constexpr int LDK = BK + V;      // padded LDS row pitch (elements)
   static constexpr int THREADS = 256;
@@ -38,6 +39,7 @@ struct Tiling {
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tiles of whole 32 x 32 blocks");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % (2 * V) == 0, "BK must cover whole MFMA k-steps");
+  static_assert(NST >= 2 && NST <= 6, "2 to 6 pipeline stages");
 };
 
 // Source of one operand tile.  K-contiguous: element (r, k) at base + r*ld + k;
@@ -317,19 +319,30 @@ struct DmaStagerT {
   }
 };
 
-// acc += B x A over K with both operands fed by DMA into two unpadded LDS
-// stages.  Iteration kt waits for its own DMA (issued one iteration earlier),
-// then a barrier makes every wave's part visible and frees the other stage,
-// which receives k-tile kt + 1 while kt is multiplied out.  An optional
-// second K segment (a2, b2, K2: same ld and rows) continues the pipeline.
+// acc += B x A over K with both operands fed by DMA into C::NST unpadded LDS
+// stages (k-tile kt in stage kt % NST).  While k-tile kt is multiplied out,
+// the DMA of the next NST - 1 k-tiles is in flight.  Before k-tile kt + 1 is
+// read each wave waits until its own DMA instructions for that tile have
+// landed (vmcnt counts vector memory instructions in issue order, so "at most
+// the later tiles' instructions outstanding" means this tile's are done),
+// then a barrier makes every wave's part visible.  The barrier for tile kt + 1
+// sits inside the last k-step of tile kt: once every wave is past it, no wave
+// reads the stage of tile kt again, so the first fragments of tile kt + 1 are
+// read while the last MFMAs of tile kt issue, and the DMA of tile kt + NST
+// refills that stage.  An optional second K segment (a2, b2, K2: same ld and
+// rows) continues the pipeline.
 template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
 MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
                           const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2,
                           const OpDesc<T>* b2, int K2) {
   constexpr int TILE_A = C::BM * C::BK, TILE_B = C::BN * C::BK;
   constexpr int STAGE = NA * TILE_A + NB * TILE_B;
+  constexpr int NST = C::NST;
   using SA = typename std::conditional<A_T, DmaStagerT<C, T, C::BM>, DmaStager<C, T, C::BM>>::type;
   using SB = typename std::conditional<B_T, DmaStagerT<C, T, C::BN>, DmaStager<C, T, C::BN>>::type;
+  // DMA instructions one wave issues per k-tile
+  constexpr int IPT = NA * SA::PER + NB * SB::PER;
+  static_assert((NST - 2) * IPT <= 63, "vmcnt range");
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
@@ -348,16 +361,38 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
     sb[i].init(b[i], tid);
     if (K2 > 0) sb[i].init_second(b2[i]);
   }
+  auto stage_of = [](int kt) { return NST == 2 ? (kt & 1) : kt % NST; };
   auto issue = [&](int kt) {
     const int seg = kt >= nk1 ? 1 : 0;
     const int k0 = (kt - seg * nk1) * C::BK;
-    T* st = smem + (kt & 1) * STAGE;
+    T* st = smem + stage_of(kt) * STAGE;
 #pragma unroll
     for (int i = 0; i < NA; ++i) sa[i].issue(st + i * TILE_A, k0, seg);
 #pragma unroll
     for (int i = 0; i < NB; ++i) sb[i].issue(st + NA * TILE_A + i * TILE_B, k0, seg);
   };
-  issue(0);
+  // wait until k-tile kt has landed, given that the k-tiles up to `last`
+  // (>= kt) have been issued: the later tiles' instructions (at most NST - 2
+  // tiles' worth) may still be outstanding
+  auto wait_tile = [&](int kt, int last) {
+    const int later = last - kt;
+    if constexpr (NST > 4) {
+      if (later >= 3) { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(3 * IPT) : "memory"); return; }
+    }
+    if constexpr (NST > 3) {
+      if (later >= 2) { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(2 * IPT) : "memory"); return; }
+    }
+    if constexpr (NST > 2) {
+      if (later >= 1) { asm volatile("s_waitcnt vmcnt(%0)" :: "n"(IPT) : "memory"); return; }
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  };
+  static_assert(NST <= 5, "wait_tile covers up to three later tiles");
+  int issued = -1;  // last k-tile whose DMA was issued
+  for (int kt = 0; kt < NST - 1 && kt < nk; ++kt) {
+    issue(kt);
+    issued = kt;
+  }
   const int frag_row = lane & 31;
   const int frag_kv = lane >> 5;
   constexpr int KSTEPS = C::BK / (2 * C::V);
@@ -381,17 +416,16 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
       }
   };
   // The compiler does not track LDS-DMA completion: every wait for a stage is
-  // an explicit vmcnt(0) followed by the barrier.  The barrier for tile kt + 1
-  // sits inside the last k-step of tile kt: once every wave has read its last
-  // fragments of stage kt & 1 and the DMA of tile kt + 1 has landed, the first
-  // fragments of tile kt + 1 are read while the last MFMAs of tile kt issue,
-  // and the DMA of tile kt + 2 refills the stage just drained.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // an explicit vmcnt followed by the barrier.
+  wait_tile(0, issued);
   __syncthreads();
-  if (nk > 1) issue(1);
+  if (NST - 1 < nk) {  // the last free stage
+    issue(NST - 1);
+    issued = NST - 1;
+  }
   read_frags(smem, smem + NA * TILE_A, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    const T* sA = smem + (kt & 1) * STAGE;
+    const T* sA = smem + stage_of(kt) * STAGE;
     const T* sB = sA + NA * TILE_A;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -399,11 +433,14 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
       if (ks + 1 < KSTEPS) {
         read_frags(sA, sB, ks + 1, cur ^ 1);
       } else if (kt + 1 < nk) {
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        wait_tile(kt + 1, issued);
         __syncthreads();
-        const T* nA = smem + ((kt + 1) & 1) * STAGE;
+        const T* nA = smem + stage_of(kt + 1) * STAGE;
         read_frags(nA, nA + NA * TILE_A, 0, cur ^ 1);
-        if (kt + 2 < nk) issue(kt + 2);
+        if (kt + NST < nk) {  // into the stage of tile kt: every wave is past it
+          issue(kt + NST);
+          issued = kt + NST;
+        }
       }
 #pragma unroll
       for (int ia = 0; ia < NA; ++ia)
@@ -428,7 +465,7 @@ constexpr int stage_elems() { return (NA * C::BM + NB * C::BN) * C::LDK; }
 // unpadded; fp32 keeps the padded pitch of the register-staged loop.
 template <class C, int NA, int NB>
 constexpr int smem_elems() {
-  return C::V == 8 ? 2 * (NA * C::BM + NB * C::BN) * C::BK : 2 * stage_elems<C, NA, NB>();
+  return C::V == 8 ? C::NST * (NA * C::BM + NB * C::BN) * C::BK : 2 * stage_elems<C, NA, NB>();
 }
 
 // acc[a * NB + b][tn][tm] += B_b-tile x A_a-tile over k in [0, K).
@@ -447,7 +484,7 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
   // DMA for every bf16 operand layout; fp32 K-major operands keep the
   // register-staged transpose below (the transposing LDS read is 16-bit)
   if constexpr (sizeof(T) == 2 || (!A_T && !B_T)) {
-    static_assert(2 * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
+    static_assert(C::NST * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
     mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, a, b, K, smem, a2, b2, K2);
     return;
   }

@@ -75,8 +75,8 @@ MOE_DEV int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 // than with 4 (their experts hold few row tiles, so pairs stay inside an
 // expert more often), config 2 unchanged; 1 was 1 % slower on configs 2 and 3,
 // 8 1.5 % slower on config 5, 3 within 0.3 % (run-to-run noise).
+template <int GM = 2>
 MOE_DEV bool tile_order(int id, int nM, int nN, int& mt, int& nt) {
-  constexpr int GM = 2;
   const int g = uni(id / (GM * nN));
   const int r = id - g * (GM * nN);
   const int gm = min(GM, nM - g * GM);
@@ -84,6 +84,22 @@ MOE_DEV bool tile_order(int id, int nM, int nN, int& mt, int& nt) {
   mt = uni(g * GM + r % gm);
   nt = uni(r / gm);
   return nt < nN;
+}
+
+// Row tiles of one group that walk down a tile column together.  A group's
+// tiles are numbered group by group (a group of R row tiles owns R x nN
+// consecutive ids) and, inside the group, bands of up to kRowWalk row tiles
+// walk down each column before moving right: the workgroups that run
+// together on an XCD then share the group's weight panel of each column
+// (every row tile of an expert multiplies the same weights) and its token-row
+// panels, instead of pairing row tiles across expert boundaries.
+constexpr int kRowWalk = 8;
+MOE_DEV void group_tile(const int* prefix, int G, int nN, int id, int& grp, int& local, int& nt) {
+  grp = uni(find_group(prefix, G, id / nN));
+  const int p0 = prefix[grp];
+  int lr;
+  tile_order<kRowWalk>(id - p0 * nN, prefix[grp + 1] - p0, nN, lr, nt);
+  local = lr;
 }
 
 // Row-grouped launches need a grid of at least 8 * ceil(tiles / 8) blocks
@@ -106,15 +122,17 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
     const int nB = g.big_prefix[g.G], nH = g.half_prefix[g.G];
     int cls;
     if (!xcd_slot2(blockIdx.x, nB * nN, nH * nN, cls, id)) return false;
-    const int* pre = cls ? g.half_prefix : g.big_prefix;
-    if (!tile_order(id, cls ? nH : nB, nN, mt, nt)) return false;
-    grp = uni(find_group(pre, g.G, mt));
-    local = cls ? -1 : mt - pre[grp];
+    if (cls) {  // one half tile per group at most: pairs down a column
+      if (!tile_order(id, nH, nN, mt, nt)) return false;
+      grp = uni(find_group(g.half_prefix, g.G, mt));
+      local = -1;
+    } else {
+      group_tile(g.big_prefix, g.G, nN, id, grp, local, nt);
+    }
   } else {  // group by group
     const int nM = g.tile_prefix[g.G];
-    if (!xcd_slot(blockIdx.x, nM * nN, id) || !tile_order(id, nM, nN, mt, nt)) return false;
-    grp = uni(find_group(g.tile_prefix, g.G, mt));
-    local = mt - g.tile_prefix[grp];
+    if (!xcd_slot(blockIdx.x, nM * nN, id)) return false;
+    group_tile(g.tile_prefix, g.G, nN, id, grp, local, nt);
   }
   n0 = nt * BN;
   const int rows = g.offsets[grp + 1] - g.offsets[grp];
@@ -643,32 +661,50 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // separate instantiation, so profiles tell the two launches apart).
 // C: the tiling (Tilings<T>::GateUp, or 128-row tiles for experts with few
 // rows, whose last row tile would otherwise be mostly padding).
-// Row-grouped tiles whose group leaves at most half of the BM rows valid (the
-// last tile of an expert) run as a BM/2-row tile with the four waves side by
-// side along N (HalfRows<C>), so every wave multiplies valid rows and the tile
-// takes about half the time; the per-element k order is unchanged, so the
-// results are the same bits.  bf16 256-row tiles only.
+// The last row tile of a group (an expert's rows past its last full tile, or
+// the dense problem's last rows) runs as the shortest of three shorter
+// tilings that covers its valid rows: BM/4 rows (QuarterRows, the four waves
+// side by side along N), BM/2 rows (HalfRows, likewise) or 3BM/4 rows
+// (ThreeQuarterRows, a 2 x 2 wave grid of 3BM/8-row blocks), so the MFMAs
+// spend no more than BM/4 rows on padding.  Config 5's ~256-row experts run
+// 79 % useful rows with BM/2 granularity and 94 % with BM/4.  Every output
+// element keeps its k order (same bits).  bf16 256-row tiles only.
 template <class C>
-using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4>;
+using QuarterRows = Tiling<bf16_t, C::BM / 4, C::BN, C::BK, 4, C::NST>;
+template <class C>
+using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4, C::NST>;
+template <class C>
+using ThreeQuarterRows = Tiling<bf16_t, 3 * C::BM / 4, C::BN, C::BK, 2, C::NST>;
 template <typename T, class C>
 constexpr bool has_half_rows() { return sizeof(T) == 2 && C::BM == 256; }
 template <typename T, class C, int NA, int NB, int NACC>
 constexpr int rowgroup_smem_elems() {
+  constexpr int a = kernel_smem_elems<C, T, NA, NB, NACC>();
   if constexpr (has_half_rows<T, C>()) {
-    constexpr int a = kernel_smem_elems<C, T, NA, NB, NACC>();
-    constexpr int b = kernel_smem_elems<HalfRows<C>, T, NA, NB, NACC>();
-    return a > b ? a : b;
+    constexpr int b = kernel_smem_elems<QuarterRows<C>, T, NA, NB, NACC>();
+    constexpr int c = kernel_smem_elems<HalfRows<C>, T, NA, NB, NACC>();
+    constexpr int d = kernel_smem_elems<ThreeQuarterRows<C>, T, NA, NB, NACC>();
+    constexpr int ab = a > b ? a : b, cd = c > d ? c : d;
+    return ab > cd ? ab : cd;
   } else {
-    return kernel_smem_elems<C, T, NA, NB, NACC>();
+    return a;
   }
 }
-// Runs body(tiling) for a resolved row tile: the half-height tiling when the
-// tile has at most BM / 2 valid rows.
+// Runs body(tiling) for a resolved row tile with mv valid rows: the shortest
+// row tiling that covers them.
 template <typename T, class C, class F>
 MOE_DEV void with_tile_rows(int mv, F&& body) {
   if constexpr (has_half_rows<T, C>()) {
+    if (mv <= C::BM / 4) {
+      body(QuarterRows<C>{});
+      return;
+    }
     if (mv <= C::BM / 2) {
       body(HalfRows<C>{});
+      return;
+    }
+    if (mv <= 3 * C::BM / 4) {
+      body(ThreeQuarterRows<C>{});
       return;
     }
   }
@@ -679,7 +715,7 @@ MOE_DEV void with_tile_rows(int mv, F&& body) {
 // 128-column tile with the four waves stacked along M (HalfCols<C>), with the
 // same per-element k order (same bits).  bf16 256-column tiles only.
 template <class C>
-using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, 1>;
+using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, 1, C::NST>;
 template <typename T, class C>
 constexpr bool has_half_cols() { return sizeof(T) == 2 && C::BN == 256; }
 template <typename T, class C, int NA, int NB, int NACC>
@@ -692,11 +728,16 @@ constexpr int rowcol_smem_elems() {
     return a;
   }
 }
-// body(tiling): half-height when at most BM / 2 rows are valid, else
-// half-width when at most BN / 2 of the nv remaining columns are valid.
+// body(tiling): a BM/4- or BM/2-row tiling when that covers the mv valid rows,
+// else the half-width tiling when at most BN / 2 of the nv remaining columns
+// are valid, else the 3BM/4-row tiling when that covers the rows, else C.
 template <typename T, class C, class F>
 MOE_DEV void with_tile_shape(int mv, int nv, F&& body) {
   if constexpr (has_half_rows<T, C>()) {
+    if (mv <= C::BM / 4) {
+      body(QuarterRows<C>{});
+      return;
+    }
     if (mv <= C::BM / 2) {
       body(HalfRows<C>{});
       return;
@@ -705,6 +746,12 @@ MOE_DEV void with_tile_shape(int mv, int nv, F&& body) {
   if constexpr (has_half_cols<T, C>()) {
     if (nv <= C::BN / 2) {
       body(HalfCols<C>{});
+      return;
+    }
+  }
+  if constexpr (has_half_rows<T, C>()) {
+    if (mv <= 3 * C::BM / 4) {
+      body(ThreeQuarterRows<C>{});
       return;
     }
   }
