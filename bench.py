@@ -2,9 +2,10 @@
 """MoE layer forward + backward throughput on one MI355X.
 
 One step = one forward and one backward pass of the MoE layer over one batch of
-synthetic tokens (every gradient written). Default workload
-(T=8192, H=2048, E=16, top-2, I=1408, shared 2816, bf16, alpha 0.01).
-Prints ONE JSON line. Other BASELINE configs: --config {1,3,4,5}.
+synthetic tokens (every gradient written). Default workload: BASELINE config 5,
+the largest configuration (T=8192, H=7168, E=256, top-8, I=2048, shared 2048,
+bf16, lognormal expert loads). Prints ONE JSON line. Other BASELINE configs:
+--config {1,2,3,4}.
 
 Inputs live in HBM before timing starts; random-init weights and N(0,1)
 activations/upstream gradients are generated on the device with a seeded
@@ -35,13 +36,14 @@ def gen_weights(torch, shape, std, gen, dtype, dev):
     return t
 
 
-def measured_traffic(workload):
-    """Bytes per launch recorded in profiles/*.md ("traffic_bytes_per_launch
-    <workload>: <bytes>"), or None."""
+def measured_traffic(workload, stage):
+    """HBM-side bytes per launch of one stage's kernel recorded in
+    profiles/*.md ("traffic_bytes_per_launch <workload> <stage>: <bytes>"), or
+    None."""
     pdir = os.path.join(ROOT, "profiles")
     if not os.path.isdir(pdir):
         return None
-    key = f"traffic_bytes_per_launch {workload}:"
+    key = f"traffic_bytes_per_launch {workload} {stage}:"
     for name in sorted(os.listdir(pdir)):
         if not name.endswith((".md", ".txt")):
             continue
@@ -53,19 +55,37 @@ def measured_traffic(workload):
 
 
 def cpu_baseline(wl, seconds, threads):
-    """The oracle (fp32, OpenMP) on a bounded sample of the same workload."""
+    """The oracle (fp32, OpenMP) on a bounded sample of the same workload: the
+    workload's H, E, k, I and S, its weight-gradient writes included, over a
+    token sample sized to take about `seconds`. With more than 16 experts the
+    expert weights are 16 distinct random sets repeated over the E experts (the
+    arithmetic and memory traffic are those of E separate experts; generating
+    E distinct sets would take minutes); if the host cannot hold the E
+    experts' weights and gradients, the sample falls back to 16 experts."""
     import numpy as np
     from oracle import moe_oracle as mo
     mo.set_threads(threads)
-    E = wl.E if wl.E <= 16 else 16   # per-token cost depends on k, H, I, S, not E
+    E = wl.E
+    need = 2 * 3 * E * wl.I * wl.H * 4 + (2 * 3 * wl.S * wl.H * 4 if wl.S else 0)
+    try:
+        import psutil
+        avail = psutil.virtual_memory().available
+    except Exception:  # noqa: BLE001 - psutil missing: assume the small sample
+        avail = 0
+    if E > 16 and avail < 1.5 * need:
+        E = 16
     k = min(wl.k, E)
     rng = np.random.default_rng(1)
 
     def normal(shape, std):
         return (rng.standard_normal(shape, dtype=np.float32) * std)
 
-    W = {"router": normal((E, wl.H), wl.w_std), "gate": normal((E, wl.I, wl.H), wl.w_std),
-         "up": normal((E, wl.I, wl.H), wl.w_std), "down": normal((E, wl.H, wl.I), wl.w_std)}
+    def experts(shape):
+        base = normal((min(E, 16),) + shape, wl.w_std)
+        return base if E <= 16 else np.tile(base, (E // 16 + 1, 1, 1))[:E].copy()
+
+    W = {"router": normal((E, wl.H), wl.w_std), "gate": experts((wl.I, wl.H)),
+         "up": experts((wl.I, wl.H)), "down": experts((wl.H, wl.I))}
     if wl.S:
         W.update(shared_gate=normal((wl.S, wl.H), wl.w_std), shared_up=normal((wl.S, wl.H), wl.w_std),
                  shared_down=normal((wl.H, wl.S), wl.w_std))
@@ -90,11 +110,17 @@ def cpu_baseline(wl, seconds, threads):
         return time.perf_counter() - t0
 
     run(32)                        # warm-up: first touch of weights and thread pool
-    t_small = run(64)
-    T = int(max(64, min(wl.T, 64 * seconds / max(t_small, 1e-6))))
+    # a call costs a fixed part (weight gradients written once) plus a part per
+    # token: fit both from two small calls, then size the sample
+    t1, t2 = run(64), run(256)
+    per_tok = max((t2 - t1) / 192, 1e-7)
+    fixed = max(t1 - 64 * per_tok, 0.0)
+    T = int(max(256, min(wl.T, (seconds - fixed) / per_tok)))
     t = run(T)
-    sample = (f"{T} tokens of the workload shape (H={wl.H}, k={k}, I={wl.I}, S={wl.S}) over "
-              f"{E} experts, oracle fp32 {'fwd+bwd' if wl.backward else 'fwd'}, {threads} threads")
+    sample = (f"{T} tokens of the workload shape (H={wl.H}, E={E}, k={k}, I={wl.I}, S={wl.S}"
+              f"{'; 16 distinct weight sets over the experts' if E > 16 else ''}), oracle fp32 "
+              f"{'fwd+bwd with every weight gradient written' if wl.backward else 'fwd'}, "
+              f"{threads} threads")
     return {"value": round(T / t, 2), "unit": "tokens/s", "cores": threads,
             "kind": "port", "sample": sample, "seconds": round(t, 3)}
 
@@ -145,7 +171,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=2, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
     ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain device copy of MIB MiB (5 launches) and exit: the "
@@ -153,7 +179,7 @@ def main():
     ap.add_argument("--achievable-peaks", action="store_true",
                     help="only measure this box's achievable peaks (library bf16 GEMMs through "
                          "torch.matmul = hipBLASLt, and a 1 GiB device copy) and exit")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--block", action="store_true",
                     help="time the block's whole MoE sub-block (post_attention_layernorm "
@@ -251,11 +277,47 @@ def main():
         else:  # forward-only call: no saved state, no gate / up pre-activations
             fwd(need_grad=False)
 
-    dominant = "gateup_fwd"
     fwd()  # realized routing (untimed)
     counts = plan.saved_field(saved, T, "counts").cpu()
+    n_touched = int((counts > 0).sum())
+    b = 2 if wl.dtype == "bf16" else 4
+    TK = T * k
+    # Algorithmic work of the single-kernel GEMM stages: flops, and HBM bytes
+    # (operands read once, outputs written once; weights of the experts that
+    # received tokens).
+    gemm_work = {
+        "gateup_fwd": (4 * TK * H * I, TK * H * b + 2 * n_touched * I * H * b + 3 * TK * I * b),
+        "down_fwd": (2 * TK * I * H, TK * I * b + n_touched * H * I * b + TK * H * b),
+        "down_dgrad": (2 * TK * H * I, TK * H * b + n_touched * H * I * b + 4 * TK * I * b),
+        "gateup_dgrad": (4 * TK * I * H, 2 * TK * I * b + 2 * n_touched * I * H * b + TK * H * b),
+        "down_wgrad": (2 * TK * H * I, TK * H * b + TK * I * b + n_touched * H * I * b),
+        "gateup_wgrad": (4 * TK * H * I, 2 * TK * I * b + TK * H * b + 2 * n_touched * I * H * b),
+    }
+    kernel_of = {
+        "gateup_fwd": f"k_gateup_fwd<{wl.dtype}, true> (grouped gate/up GEMM + SwiGLU)",
+        "down_fwd": f"k_down_fwd<{wl.dtype}, true> (grouped down projection)",
+        "down_dgrad": f"k_down_dgrad<{wl.dtype}, true> (grouped input gradient of down + SwiGLU backward)",
+        "gateup_dgrad": f"k_gateup_dgrad<{wl.dtype}, true> (grouped input gradient of gate/up)",
+        "down_wgrad": f"k_wgrad<{wl.dtype}, 1, true> (grouped down weight gradient)",
+        "gateup_wgrad": f"k_wgrad<{wl.dtype}, 2, true> (grouped gate/up weight gradient)",
+    }
+    peak_mfma = PEAK_FP32_TFLOPS if wl.dtype == "f32" else PEAK_BF16_TFLOPS
+    ridge = peak_mfma * 1e12 / (PEAK_HBM_GBS * 1e9)   # flop per HBM byte
     for _ in range(args.warmup):
         step()
+    torch.cuda.synchronize()
+    if wl.backward:
+        # the kernel with the most GPU time in the overlapped steps: every
+        # stage evented on its own stream during two extra untimed steps
+        plan.stage_times(reset=True)
+        plan.set_profiling(list(gemm_work))
+        for _ in range(2):
+            step()
+        insitu = {n: ms / c for n, (ms, c) in plan.stage_times(reset=True).items() if c}
+        dominant = max((n for n in gemm_work if n in insitu), key=lambda n: insitu[n])
+    else:  # forward-only small-token path: the gate/up weight stream
+        dominant = "gateup_fwd"
+    plan.set_profiling([])
     torch.cuda.synchronize()
     plan.stage_times(reset=True)
     plan.set_profiling([dominant])
@@ -279,18 +341,12 @@ def main():
 
     ms_per_step = elapsed * 1e3 / args.steps
     tok_s = T / (elapsed / args.steps)
-    TK = T * k
     fwd_flops = 2 * T * H * E + 6 * TK * H * I + 6 * T * H * S
     total_flops = fwd_flops * (3 if wl.backward else 1)
     dom_avg_ms = dom_ms / max(dom_calls, 1)
-    n_touched = int((counts > 0).sum())
-    if wl.dtype == "f32":
-        peak, bound = PEAK_FP32_TFLOPS, "mfma"
-    else:
-        peak, bound = PEAK_BF16_TFLOPS, "mfma"
-    dom_flops = 4 * TK * H * I
+    peak = peak_mfma
+    extra = {}
     if not wl.backward:  # small-token forward: HBM bound on the expert weights touched
-        b = 2
         dom_bytes = n_touched * 2 * H * I * b + TK * H * b + TK * I * b
         roof = {"bound": "hbm", "achieved": round(dom_bytes / (dom_avg_ms * 1e-3) / 1e9, 1),
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
@@ -298,27 +354,41 @@ def main():
         layer_bytes = (n_touched * 3 * H * I * b + E * H * b + 2 * T * H * b + T * E * 4 + TK * 8)
         extra = {"layer_hbm_GBs": round(layer_bytes / (elapsed / args.steps) / 1e9, 1),
                  "layer_hbm_frac": round(layer_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4)}
-    else:
-        ach = dom_flops / (dom_avg_ms * 1e-3) / 1e12
-        roof = {"bound": bound, "achieved": round(ach, 1), "peak": peak, "unit": "TFLOP/s",
-                "frac": round(ach / peak, 4)}
-        iso = dom_flops / (stages[dominant] * 1e-3) / 1e12
-        extra = {"dominant_kernel_serial": {"achieved": round(iso, 1), "frac": round(iso / peak, 4),
-                                            "ms": round(stages[dominant], 4)}}
-    # HBM-side bytes per launch of this kernel and workload, as measured by the
-    # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel) that
-    # are summarised under profiles/; null when no such measurement exists.
-    roof["traffic"] = measured_traffic(wl.name)
-    if wl.dtype == "bf16" and T <= 64:   # small-token path: weight-streaming kernels
         roof["kernel"] = (f"k_skinny_fwd<true, false> (gate/up weight stream + SwiGLU), "
                           f"{dom_avg_ms:.4f} ms/launch")
     else:
-        roof["kernel"] = (f"k_gateup_fwd<{'bf16' if wl.dtype == 'bf16' else 'f32'}, true> "
-                          f"(grouped gate/up GEMM + SwiGLU), {dom_avg_ms:.4f} ms/launch")
+        flops, nbytes = gemm_work[dominant]
+        tflops = flops / (dom_avg_ms * 1e-3) / 1e12
+        gbs = nbytes / (dom_avg_ms * 1e-3) / 1e9
+        mfma_side = {"achieved": round(tflops, 1), "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(tflops / peak, 4)}
+        hbm_side = {"achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                    "frac": round(gbs / PEAK_HBM_GBS, 4)}
+        # the roof that binds: HBM below the ridge intensity, MFMA above it
+        intensity = flops / nbytes
+        if intensity < ridge:
+            roof = {"bound": "hbm", **hbm_side}
+            extra["roofline_mfma_side"] = mfma_side
+        else:
+            roof = {"bound": "mfma", **mfma_side}
+            extra["roofline_hbm_side"] = hbm_side
+        roof["kernel"] = f"{kernel_of[dominant]}, {dom_avg_ms:.4f} ms/launch"
+        roof["stage"] = dominant
+        roof["flop_per_launch"] = flops
+        roof["bytes_per_launch"] = nbytes
+        roof["intensity_flop_per_byte"] = round(intensity, 1)
+        iso_ms = stages[dominant]
+        extra["dominant_kernel_serial"] = {"ms": round(iso_ms, 4),
+                                           "TFLOP/s": round(flops / (iso_ms * 1e-3) / 1e12, 1),
+                                           "GB/s": round(nbytes / (iso_ms * 1e-3) / 1e9, 1)}
+        extra["insitu_stage_ms"] = {n: round(v, 4) for n, v in insitu.items()}
+    # HBM-side bytes per launch of this kernel and workload, as measured by the
+    # rocprofv3 FETCH_SIZE / WRITE_SIZE passes (scaled by a copy kernel) that
+    # are summarised under profiles/; null when no such measurement exists.
+    roof["traffic"] = measured_traffic(wl.name, dominant)
 
     # memory-bound stages against the HBM roofline: algorithmic bytes per call
     # (b = element size) over the serial stage time of the profiling steps
-    b = 2 if wl.dtype == "bf16" else 4
     stage_bytes = {
         "router_gemm": T * H * b + E * H * b + T * E * 4,
         "route": 3 * T * E * 4 + T * 4 + TK * 8,

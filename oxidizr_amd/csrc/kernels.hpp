@@ -66,6 +66,17 @@ struct RowGroups {
 // scalar registers so that the address arithmetic built on them stays scalar.
 MOE_DEV int uni(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Waves of the router kernels that split the hidden dimension (k_router_small,
+// k_router_route).
+constexpr int kRouterWaves = 16;
+
+// 16 x 16 x 32 bf16 MFMA: acc[r] of lane l = sum_k a[row 4 (l / 16) + r][k] * b[row l % 16][k]
+// with lane l supplying k-vector 8 (l / 16) (+ 32 q per step) of a-row and b-row l % 16.
+MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
+}
+
 // Output-tile order.  Workgroup ids are first made contiguous per XCD
 // (xcd_slot); consecutive ids then walk GM row-tiles down a tile column
 // before moving one column right, so the ~32 workgroups resident on one XCD
@@ -239,12 +250,17 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
 // ------------------------------------------------------------------ routing
 // One wave routes token t: softmax(logits / tau), log-sum-exp, top-k on the
 // raw logits (NaN selects as -inf; equal values -> lower expert index first).
+// `row` holds the token's E logits (global memory, or a row staged in LDS by
+// the fused router kernel): the same arithmetic either way, so the same bits.
+// Also returns, in registers, the lane's probabilities pr[i] (expert
+// lane + 64 i, 0 past E) and the chosen experts sel[0..k) (the same in every
+// lane).
 template <int EPL>
-MOE_DEV void route_one(const float* __restrict__ logits, int t, int E, int k, float tau,
+MOE_DEV void route_row(const float* row, int t, int E, int k, float tau,
                        int norm, float* __restrict__ probs, float* __restrict__ lse,
-                       int* __restrict__ idx, float* __restrict__ w) {
+                       int* __restrict__ idx, float* __restrict__ w, float (&pr)[EPL],
+                       int (&sel)[16]) {
   const int lane = threadIdx.x & 63;
-  const float* row = logits + (int64_t)t * E;
   float v[EPL], ex[EPL];
   float mx = -INFINITY;
 #pragma unroll
@@ -265,7 +281,8 @@ MOE_DEV void route_one(const float* __restrict__ logits, int t, int E, int k, fl
 #pragma unroll
   for (int i = 0; i < EPL; ++i) {
     const int e = lane + 64 * i;
-    if (e < E) probs[(int64_t)t * E + e] = ex[i] / s;
+    pr[i] = e < E ? ex[i] / s : 0.0f;
+    if (e < E) probs[(int64_t)t * E + e] = pr[i];
   }
   if (lane == 0) lse[t] = mx + logf(s);
 
@@ -306,6 +323,7 @@ MOE_DEV void route_one(const float* __restrict__ logits, int t, int E, int k, fl
     const float pj = __shfl(mine, be & 63, 64) / s;
     wsel[j] = pj;
     isel[j] = be;
+    sel[j] = be;
     wsum += pj;
   }
   if (lane == 0) {
@@ -324,7 +342,134 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
                                                int* __restrict__ idx, float* __restrict__ w) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
-  route_one<EPL>(logits, t, E, k, tau, norm, probs, lse, idx, w);
+  float pr[EPL];
+  int sel[16];
+  route_row<EPL>(logits + (int64_t)t * E, t, E, k, tau, norm, probs, lse, idx, w, pr, sel);
+}
+
+// ------------------------------------------------------------------ fused router
+// Router GEMM, softmax, log-sum-exp and top-k in one launch (bf16, up to
+// kFusedRouterMaxExperts experts).  A workgroup of kRouterWaves waves owns 16
+// tokens and every expert (NEB = ceil(E / 16) blocks of 16): as in
+// k_router_small each wave takes every kRouterWaves-th 256-wide k-chunk of the
+// hidden dimension and multiplies its 16 token rows with the NEB router-row
+// blocks (v_mfma_f32_16x16x32_bf16), the partial sums are added through LDS in
+// wave order, and each of the 16 waves then routes one token with route_row
+// (the arithmetic of k_route) from the logits row staged in LDS.
+constexpr int kFusedRouterMaxExperts = 64;
+// The workgroup also writes what the dispatch and the losses need from its 16
+// tokens: the expert histogram of their k choices (group_hist[b][e], an
+// integer LDS histogram) and the column sums of their probabilities
+// (prob_part[b][e], tokens added in order), so that k_scan over the 16-token
+// groups and k_colsum_final finish the counts, offsets and P.
+template <int NEB>
+__global__ __launch_bounds__(64 * kRouterWaves) void k_router_route(
+    const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, const float* __restrict__ bias,
+    int Tn, int H, int E, int k, float tau, int norm, float* __restrict__ logits,
+    float* __restrict__ probs, float* __restrict__ lse, int* __restrict__ idx,
+    float* __restrict__ w, int* __restrict__ group_hist, float* __restrict__ prob_part) {
+  static_assert(16 * NEB <= kFusedRouterMaxExperts, "expert blocks");
+  __shared__ f32x4 red[kRouterWaves][NEB][64];
+  __shared__ float lg[16][16 * NEB + 4];
+  __shared__ float pl[16][64];  // probabilities of the group's tokens
+  __shared__ int hist[16 * NEB];
+  const int t0 = blockIdx.x * 16;
+  const int wave = uni(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int g = lane >> 4, rl = lane & 15;
+  const int ntok = min(16, Tn - t0);
+  const rsrc_t rx = make_rsrc(x + (int64_t)t0 * H, (uint32_t)((int64_t)ntok * H * 2));
+  const rsrc_t rw = make_rsrc(wr, (uint32_t)((int64_t)E * H * 2));
+  const uint32_t vx = (uint32_t)((rl * H + 8 * g) * 2);
+  f32x4 acc[NEB];
+#pragma unroll
+  for (int b = 0; b < NEB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  for (int kc = wave; kc * 256 < H; kc += kRouterWaves) {
+    const uint32_t soff = (uint32_t)kc * 512;
+    u32x4 xa[8], wa[NEB][8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const bool kin = kc * 256 + 32 * q + 8 * g < H;
+      xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
+#pragma unroll
+      for (int b = 0; b < NEB; ++b) {
+        const uint32_t vw = (uint32_t)(((b * 16 + rl) * H + 8 * g) * 2);
+        wa[b][q] = buf_ld16(rw, kin && b * 16 + rl < E ? vw + 64 * q : kOobOffset, soff);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+#pragma unroll
+      for (int b = 0; b < NEB; ++b) mfma16(acc[b], xa[q], wa[b][q]);
+  }
+#pragma unroll
+  for (int b = 0; b < NEB; ++b) red[wave][b][lane] = acc[b];
+  __syncthreads();
+  // wave b < NEB adds expert block b over the waves in order; lane holds
+  // D[token 4 g + r][expert 16 b + rl]
+  if (wave < NEB) {
+    const int e = wave * 16 + rl;
+    f32x4 v = red[0][wave][lane];
+#pragma unroll
+    for (int q = 1; q < kRouterWaves; ++q) v += red[q][wave][lane];
+    const float bv = e < E && bias ? bias[e] : 0.0f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) lg[4 * g + r][e] = v[r] + bv;
+  }
+  if (threadIdx.x < 16 * NEB) hist[threadIdx.x] = 0;
+  __syncthreads();
+  if (wave < ntok) {
+    const int t = t0 + wave;
+    for (int e = lane; e < E; e += 64) logits[(int64_t)t * E + e] = lg[wave][e];
+    float pr[1];
+    int sel[16];
+    route_row<1>(&lg[wave][0], t, E, k, tau, norm, probs, lse, idx, w, pr, sel);
+    pl[wave][lane] = pr[0];
+    if (lane == 0)
+      for (int j = 0; j < k; ++j) atomicAdd(&hist[sel[j]], 1);
+  }
+  __syncthreads();
+  // the group's histogram and probability column sums (tokens in order)
+  const int b = blockIdx.x;
+  if (threadIdx.x < E) {
+    const int e = threadIdx.x;
+    group_hist[(int64_t)b * E + e] = hist[e];
+    float sum = 0.0f;
+    for (int i = 0; i < ntok; ++i) sum += pl[i][e];
+    prob_part[(int64_t)b * E + e] = sum;
+  }
+}
+
+// Stable scatter over 16-token groups (the groups of k_router_route, whose
+// bases k_scan computed): the position of assignment (t, j) is the base of its
+// group and expert plus the number of earlier tokens of the group that chose
+// the same expert, read from a 16-bit token mask per (group, expert) built with
+// LDS atomic ORs (order-independent).  256 threads = 16 groups; E <= 64.
+__global__ __launch_bounds__(256) void k_scatter16(const int* __restrict__ idx, int Tn, int k,
+                                                   int E, const int* __restrict__ group_base,
+                                                   int* __restrict__ perm,
+                                                   int* __restrict__ inv_perm) {
+  __shared__ unsigned mask[16][kFusedRouterMaxExperts];
+  const int tid = threadIdx.x;
+  const int t = blockIdx.x * 256 + tid;
+  const int gl = tid >> 4, r = tid & 15;  // local group, rank of the token in it
+  for (int i = tid; i < 16 * kFusedRouterMaxExperts; i += 256) (&mask[0][0])[i] = 0u;
+  __syncthreads();
+  const bool valid = t < Tn;
+  int keys[16];
+  for (int j = 0; j < k; ++j) {
+    keys[j] = valid ? idx[(int64_t)t * k + j] : 0;
+    if (valid) atomicOr(&mask[gl][keys[j]], 1u << r);
+  }
+  __syncthreads();
+  if (!valid) return;
+  const int grp = t >> 4;
+  const unsigned below = (1u << r) - 1u;
+  for (int j = 0; j < k; ++j) {
+    const int e = keys[j];
+    const int pos = group_base[(int64_t)grp * E + e] + __popc(mask[gl][e] & below);
+    perm[pos] = t * k + j;
+    inv_perm[(int64_t)t * k + j] = pos;
+  }
 }
 
 // ------------------------------------------------------------------ column sums
@@ -492,8 +637,19 @@ __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_his
   const bool act = g < G;
   const int chunk = (nb + G - 1) / G;
   const int b0 = act ? g * chunk : 0, b1 = act ? min(nb, b0 + chunk) : 0;
+  // eight independent loads in flight per step (many blocks: the fused
+  // router's 16-token groups)
+  constexpr int U = 8;
   int sum = 0;
-  for (int b = b0; b < b1; ++b) sum += block_hist[(int64_t)b * E + e];
+  int b = b0;
+  for (; b + U <= b1; b += U) {
+    int c[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) c[u] = block_hist[(int64_t)(b + u) * E + e];
+#pragma unroll
+    for (int u = 0; u < U; ++u) sum += c[u];
+  }
+  for (; b < b1; ++b) sum += block_hist[(int64_t)b * E + e];
   part[tid] = sum;
   __syncthreads();
   if (tid < E) {
@@ -510,7 +666,18 @@ __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_his
   scan_counts(cnt, E, offsets, tile_prefix, offs, wsum);
   if (act) {
     int run = offs[e] + part[tid];
-    for (int b = b0; b < b1; ++b) {
+    int b = b0;
+    for (; b + U <= b1; b += U) {
+      int c[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) c[u] = block_hist[(int64_t)(b + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        block_base[(int64_t)(b + u) * E + e] = run;
+        run += c[u];
+      }
+    }
+    for (; b < b1; ++b) {
       const int c = block_hist[(int64_t)b * E + e];
       block_base[(int64_t)b * E + e] = run;
       run += c;
@@ -1397,10 +1564,6 @@ __global__ __launch_bounds__(256) void k_rowsum(const float* __restrict__ in, in
 constexpr int kSkinnyMaxTokens = 64;
 constexpr int kSkinnyRows = 64;  // weight rows (output columns) per workgroup
 
-MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b) {
-  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
-}
 
 // A pointer every lane holds, moved to scalar registers: buffer resources
 // built from it then stay scalar (a resource the compiler cannot prove uniform
@@ -1550,7 +1713,6 @@ __global__ __launch_bounds__(256) void k_skinny_fwd(const bf16_t* __restrict__ X
 // the launch is small, so the work is cut finely (H = 4096: one chunk per
 // wave, 16 token rows per workgroup): one CU cannot pull the whole token
 // matrix quickly.
-constexpr int kRouterWaves = 16;
 __global__ __launch_bounds__(64 * kRouterWaves) void k_router_small(const bf16_t* __restrict__ x,
                                                       const bf16_t* __restrict__ wr,
                                                       const float* __restrict__ bias,

@@ -66,7 +66,7 @@ struct SavedLayout {
 
 struct WsLayout {
   // forward
-  size_t block_hist, block_base, colpart, sY, infer;
+  size_t block_hist, block_base, colpart, ghist, gbase, gpart, sY, infer;
   // backward
   size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
       recomp, dxm, dwn, dwn_a, dwn_b;
@@ -74,6 +74,18 @@ struct WsLayout {
 };
 
 int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
+
+// The fused router kernel (router GEMM + routing + the 16-token groups'
+// histograms and probability sums) applies to bf16 plans with up to
+// kFusedRouterMaxExperts experts and more than kRouteSmallTokens tokens (the
+// small-token path keeps k_router_small, whose 16 x 16 blocks spread a few
+// tokens over more workgroups).  With more experts a workgroup that owns every
+// expert of its tokens re-reads the whole router weight per 16 tokens; there
+// the tiled router GEMM and k_route stay separate.
+bool fused_router(const moe_config& c, int64_t T) {
+  return c.dtype == MOE_DTYPE_BF16 && c.num_experts <= kFusedRouterMaxExperts &&
+         T > kRouteSmallTokens;
+}
 // Buffer loads take 32-bit byte offsets and kOobOffset (2^31) must lie beyond
 // every resource: no operand extent may reach this many bytes.
 constexpr int64_t kMaxExtentBytes = int64_t(1) << 31;
@@ -169,9 +181,9 @@ struct moe_plan {
   // only by the losses) while the call's stream dispatches.
   hipStream_t wgs = nullptr;
   hipEvent_t wfork = nullptr, wmid = nullptr, wjoin = nullptr;
-  bool overlap = true;
+  int overlap = 1;  // 0: serial; 1: shared-expert and weight-gradient streams; 2: shared only
   hipStream_t shared_stream(hipStream_t s) const { return overlap && aux ? aux : s; }
-  hipStream_t wgrad_stream(hipStream_t s) const { return overlap && wgs ? wgs : s; }
+  hipStream_t wgrad_stream(hipStream_t s) const { return overlap == 1 && wgs ? wgs : s; }
 
   int E() const { return cfg.num_experts; }
   int es() const { return elt_size(cfg.dtype); }
@@ -235,6 +247,12 @@ struct moe_plan {
     L.block_hist = f.take(4 * (size_t)nb * E);
     L.block_base = f.take(4 * (size_t)nb * E);
     L.colpart = f.take(4 * (size_t)nrb * E);
+    // fused router: per 16-token group histograms, dispatch bases and
+    // probability column sums
+    const size_t ng = fused_router(cfg, T) ? (size_t)ceil_div(T, 16) * E : 0;
+    L.ghist = f.take(4 * ng);
+    L.gbase = f.take(4 * ng);
+    L.gpart = f.take(4 * ng);
     L.sY = f.take(b * T * H);
     // forward-only calls keep their routing and activations here, clear of
     // the forward scratch above (the backward regions below are unused then)
@@ -401,9 +419,22 @@ void launch_route(hipStream_t s, int grid, const float* logits, int T, int E, in
 // pjoin != null: the mean probabilities P may be summed on the plan's
 // weight-gradient stream, forked through *pjoin; the caller joins it before
 // reading P.
+
+template <int NEB>
+void launch_router_route(hipStream_t s, int T, const bf16_t* x, const bf16_t* wr, const float* b,
+                         int H, int E, int k, float tau, int norm, float* logits, float* probs,
+                         float* lse, int* idx, float* w, int* ghist, float* gpart) {
+  hipLaunchKernelGGL((k_router_route<NEB>), dim3(ceil_div(T, 16)), dim3(64 * kRouterWaves), 0, s,
+                     x, wr, b, T, H, E, k, tau, norm, logits, probs, lse, idx, w, ghist, gpart);
+}
+
+// Routing (from logits already in saved, unless `routed`: the fused router
+// kernel has written the routing decisions too), losses' P statistics and
+// dispatch.
 template <typename D>
 moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
-                       const SavedLayout& L, const WsLayout& W, SideJoin* pjoin) {
+                       const SavedLayout& L, const WsLayout& W, SideJoin* pjoin,
+                       bool routed = false) {
   const moe_config& c = p->cfg;
   const int T = (int)T64, E = c.num_experts, k = c.experts_per_tok;
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
@@ -421,7 +452,7 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
     StageTimer st(p, s, MOE_STAGE_ROUTE);
     const int grid = ceil_div(T, 4);
     const float tau = c.router_temperature;
-    switch (route_epl(E)) {
+    if (!routed) switch (route_epl(E)) {
       case 1: launch_route<1>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
       case 2: launch_route<2>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
       case 4: launch_route<4>(s, grid, logits, T, E, k, tau, c.norm_topk_prob, probs, lse, idx, w); break;
@@ -435,25 +466,43 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
       LAUNCH_CHECK();
       return MOE_OK;
     }
-    const int nrb = ceil_div(T, 64);
-    float* part = (float*)(ws + W.colpart);
     const hipStream_t ps = pjoin ? p->wgrad_stream(s) : s;
     if (pjoin) HIP_TRY(pjoin->fork(s, ps, p->wfork, p->wjoin));
-    hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps, probs, T,
-                       E, part);
-    hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ps, part, nrb, E,
-                       1.0f / (float)T, P);
+    if (routed) {  // P from the fused router's per-group sums, in two fixed-order levels
+      const int ng = ceil_div(T, 16), nrb = ceil_div(ng, 64);
+      float* part = (float*)(ws + W.colpart);
+      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps,
+                         (const float*)(ws + W.gpart), ng, E, part);
+      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ps, part, nrb, E,
+                         1.0f / (float)T, P);
+    } else {
+      const int nrb = ceil_div(T, 64);
+      float* part = (float*)(ws + W.colpart);
+      hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps, probs,
+                         T, E, part);
+      hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ps, part, nrb, E,
+                         1.0f / (float)T, P);
+    }
     LAUNCH_CHECK();
   }
   {
     StageTimer st(p, s, MOE_STAGE_DISPATCH);
-    const int nb = ceil_div(T, 256);
-    int* bh = (int*)(ws + W.block_hist);
-    int* bb = (int*)(ws + W.block_base);
-    hipLaunchKernelGGL(k_hist, dim3(nb), dim3(256), sizeof(int) * E, s, idx, T, k, E, bh);
-    hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bh, nb, E, bb, counts, offsets, tprefix);
-    hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), sizeof(int) * 16 * E, s, idx, T, k, E,
-                       bb, perm, inv);
+    if (routed) {  // the fused router counted its 16-token groups' choices
+      const int ng = ceil_div(T, 16);
+      int* gb = (int*)(ws + W.gbase);
+      hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, (const int*)(ws + W.ghist), ng, E, gb,
+                         counts, offsets, tprefix);
+      hipLaunchKernelGGL(k_scatter16, dim3(ceil_div(T, 256)), dim3(256), 0, s, idx, T, k, E, gb,
+                         perm, inv);
+    } else {
+      const int nb = ceil_div(T, 256);
+      int* bh = (int*)(ws + W.block_hist);
+      int* bb = (int*)(ws + W.block_base);
+      hipLaunchKernelGGL(k_hist, dim3(nb), dim3(256), sizeof(int) * E, s, idx, T, k, E, bh);
+      hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, bh, nb, E, bb, counts, offsets, tprefix);
+      hipLaunchKernelGGL(k_scatter, dim3(nb), dim3(256), sizeof(int) * 16 * E, s, idx, T, k, E,
+                         bb, perm, inv);
+    }
     LAUNCH_CHECK();
   }
   return MOE_OK;
@@ -693,9 +742,24 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     shared_fwd<D>(p, ss, T, x, w, st.sG, st.sU, st.sA, sY);
     LAUNCH_CHECK();
   }
+  const bool fused = fused_router(c, T64);
   {
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
-    if (std::is_same<D, bf16_t>::value && (T <= kSkinnyMaxTokens || E <= kRouterSmallMaxExperts)) {
+    if (fused) {  // router GEMM, softmax, lse and top-k in one launch
+      const bf16_t* xb = (const bf16_t*)x;
+      const bf16_t* wrb = (const bf16_t*)w->router;
+      const float* rbias = c.has_router_bias ? w->router_bias : nullptr;
+      const float tau = c.router_temperature;
+      const int nt = c.norm_topk_prob;
+      int* gh = (int*)(ws + W.ghist);
+      float* gp = (float*)(ws + W.gpart);
+      if (E <= 16)
+        launch_router_route<1>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
+      else if (E <= 32)
+        launch_router_route<2>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
+      else
+        launch_router_route<4>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
+    } else if (std::is_same<D, bf16_t>::value && (T <= kSkinnyMaxTokens || E <= kRouterSmallMaxExperts)) {
       hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16) * ceil_div(T, 16)),
                          dim3(64 * kRouterWaves), 0, s, (const bf16_t*)x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
@@ -707,7 +771,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join);
+  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused);
   if (r != MOE_OK) return r;
   {
     // beside the dispatch when P is summed on the side stream (the kernel
@@ -1370,7 +1434,8 @@ moe_status moe_plan_set_profiling(moe_plan* p, int32_t stage_mask) {
 moe_status moe_plan_set_shared_overlap(moe_plan* p, int32_t on) {
   moe_status st = check_plan(p);
   if (st != MOE_OK) return st;
-  p->overlap = on != 0;
+  if (on < 0 || on > 2) return fail(MOE_ERR_INVALID, "overlap mode %d is not 0, 1 or 2", on);
+  p->overlap = on;
   return MOE_OK;
 }
 

@@ -301,9 +301,11 @@ class Plan:
         _lib.check(L.moe_plan_set_profiling(self.h, mask))
 
     def set_shared_overlap(self, on=True):
-        """Run the shared expert on the plan's second stream (default) or in
-        serial order on the call's stream."""
-        _lib.check(_lib.load().moe_plan_set_shared_overlap(self.h, int(bool(on))))
+        """Side streams of the plan: True / 1 (default) runs the shared expert
+        and the routed weight gradients on streams of their own; 2 the shared
+        expert only; False / 0 everything in serial order on the call's
+        stream."""
+        _lib.check(_lib.load().moe_plan_set_shared_overlap(self.h, int(on)))
 
     def stage_times(self, reset=True):
         ms = (ctypes.c_float * _lib.NUM_STAGES)()

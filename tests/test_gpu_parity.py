@@ -141,6 +141,8 @@ BF16_CASES = [
     dict(T=1280, H=136, E=4, k=2, I=200, S=0, half_last=True),
     # k above what dx prefetches per row group (bf16: 8)
     dict(T=160, H=64, E=12, k=10, I=48, S=16),
+    # fused router with a partial last expert block (E = 40) and router bias
+    dict(T=300, H=200, E=40, k=4, I=64, S=0, bias=True),
 ]
 
 
