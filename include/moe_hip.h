@@ -138,6 +138,19 @@ moe_status moe_forward(moe_plan* plan, void* stream, int64_t num_tokens, const v
                        const moe_weights* w, void* out, float* aux_loss, float* z_loss,
                        void* saved, void* workspace);
 
+/* Forward-only call (as moe_forward with saved == NULL) that allocates
+ * nothing: its scratch is a static device array of the library, 64 MiB per
+ * GPU (held until the process ends), instead of a caller workspace, and it
+ * creates no events (per-stage profiling is skipped for it).  Returns
+ * MOE_ERR_UNSUPPORTED when num_tokens needs more scratch than that (the
+ * forward regions of moe_workspace_bytes; decode-sized batches fit).  Every
+ * call on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (other streams, other plans, other threads) race; order them.  No
+ * counterpart in the reference: for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops). */
+moe_status moe_forward_noalloc(moe_plan* plan, void* stream, int64_t num_tokens, const void* x,
+                               const moe_weights* w, void* out, float* aux_loss, float* z_loss);
+
 /* Backward of the forward that filled `saved` (same x, weights, num_tokens).
  * d_out [T, H]; d_aux, d_z: device fp32 scalars dL/d(aux_loss), dL/d(z_loss)
  * (the trainer's alpha/n and gamma/n, src/trainer.rs:399-421), or NULL for 0.

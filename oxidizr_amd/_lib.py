@@ -21,7 +21,7 @@ EXPORTED = [
     "moe_workspace_bytes", "moe_forward", "moe_backward", "moe_route_from_logits",
     "moe_saved_field_range", "moe_stage_name", "moe_plan_set_profiling", "moe_plan_stage_times",
     "moe_plan_set_shared_overlap", "moe_block_forward", "moe_block_backward",
-    "moe_last_error", "moe_version", "moe_check_tokens",
+    "moe_last_error", "moe_version", "moe_check_tokens", "moe_forward_noalloc",
 ]
 NUM_STAGES = 20
 
@@ -86,6 +86,8 @@ def load():
     L.moe_workspace_bytes.restype = sz
     L.moe_forward.argtypes = [_vp, _vp, i64, _vp, P(MoeWeightsC), _vp, _vp, _vp, _vp, _vp]
     L.moe_forward.restype = i32
+    L.moe_forward_noalloc.argtypes = [_vp, _vp, i64, _vp, P(MoeWeightsC), _vp, _vp, _vp]
+    L.moe_forward_noalloc.restype = i32
     L.moe_backward.argtypes = [_vp, _vp, i64, _vp, _vp, _vp, _vp, P(MoeWeightsC), _vp, _vp, _vp,
                                P(MoeGradsC), _vp]
     L.moe_backward.restype = i32

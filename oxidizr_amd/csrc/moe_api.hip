@@ -4,6 +4,7 @@
 #include <cstdio>
 #include <algorithm>
 #include <cstring>
+#include <mutex>
 #include <new>
 #include <string>
 #include <vector>
@@ -71,6 +72,7 @@ struct WsLayout {
   size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
       recomp, dxm, dwn, dwn_a, dwn_b;
   size_t total;
+  size_t fwd_total;  // bytes a forward-only call touches (the forward regions)
 };
 
 int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
@@ -148,9 +150,17 @@ size_t splitk_bytes(const moe_config& c, int64_t T, bool shared) {
 
 }  // namespace
 
+// Scratch of moe_forward_noalloc: a static device array standing in for the
+// caller's workspace (one copy per GPU, held until the process ends).  Host
+// code never passes the array's name to a kernel: its device address, per
+// device, comes from hipGetSymbolAddress at plan creation (resolve_scratch).
+constexpr size_t kNoAllocScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
 struct moe_plan {
   moe_config cfg;
   int device;
+  void* scratch_ptr = nullptr;  // device address of `scratch` on this plan's device
   // device pointer tables: 0 gate, 1 up, 2 down (weights); 3..5 their grads
   void** d_tab = nullptr;
   // Pinned host staging for table uploads: a ring of kTabSlots slots of 6 E
@@ -285,6 +295,7 @@ struct moe_plan {
     L.dwn_a = g.take(blk ? 4 * (size_t)ceil_div(nrow, 16) * H : 0);
     L.dwn_b = g.take(blk ? 4 * (size_t)ceil_div(nrow, 256) * H : 0);
     L.total = f.off > g.off ? f.off : g.off;
+    L.fwd_total = f.off;
     return L;
   }
 
@@ -987,6 +998,28 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   return MOE_OK;
 }
 
+// Device addresses of `scratch`, one per device, resolved once per device
+// (with that device current) and kept for the life of the process.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+moe_status resolve_scratch(int device, void** out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (device < 0 || device >= kMaxScratchDevices)
+    return fail(MOE_ERR_UNSUPPORTED, "device %d: no static scratch slot", device);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(MOE_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", device,
+                  hipGetErrorString(e));
+    g_scratch_ptr[device] = ptr;
+  }
+  *out = g_scratch_ptr[device];
+  return MOE_OK;
+}
+
 moe_status check_plan(const moe_plan* p) {
   if (!p) return fail(MOE_ERR_INVALID, "plan is NULL");
   return MOE_OK;
@@ -1094,6 +1127,11 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
   if (!p) return fail(MOE_ERR_OOM, "host allocation of the plan failed");
   p->cfg = *cfg;
   p->device = device;
+  // the static scratch of moe_forward_noalloc on this device (device current)
+  if (resolve_scratch(device, &p->scratch_ptr) != MOE_OK) {
+    delete p;
+    return MOE_ERR_HIP;
+  }
   const size_t tab_bytes = sizeof(void*) * 6 * (size_t)cfg->num_experts;
   hipError_t e = hipMalloc((void**)&p->d_tab, tab_bytes);
   if (e == hipSuccess)
@@ -1394,6 +1432,27 @@ moe_status moe_block_backward(moe_plan* p, void* stream, int64_t T, const void* 
                               uint8_t* has_grad) {
   return backward_entry(p, stream, T, d_out, d_aux, d_z, h, norm_weight, w, saved, workspace,
                         dh, d_norm_weight, g, has_grad, true);
+}
+
+moe_status moe_forward_noalloc(moe_plan* p, void* stream, int64_t T, const void* x,
+                               const moe_weights* w, void* out, float* aux_loss, float* z_loss) {
+  moe_status st = check_plan(p);
+  if (st != MOE_OK) return st;
+  if ((st = check_tokens(p, T)) != MOE_OK) return st;
+  if (!p->scratch_ptr) return fail(MOE_ERR_HIP, "the plan has no static scratch");
+  const size_t need = p->ws_layout(T).fwd_total;
+  if (need > kNoAllocScratchBytes)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "moe_forward_noalloc: %lld tokens need %zu bytes of scratch, above the %zu-byte "
+                "static scratch; call moe_forward with a workspace",
+                (long long)T, need, kNoAllocScratchBytes);
+  // no per-stage events: creating them could allocate
+  const uint32_t mask = p->profile_mask;
+  p->profile_mask = 0;
+  st = forward_entry(p, stream, T, x, nullptr, w, out, aux_loss, z_loss, nullptr, p->scratch_ptr,
+                     false);
+  p->profile_mask = mask;
+  return st;
 }
 
 moe_status moe_route_from_logits(moe_plan* p, void* stream, int64_t T, const float* logits,

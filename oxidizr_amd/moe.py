@@ -235,6 +235,14 @@ class Plan:
                                            _p(out), _p(aux), _p(z), _p(saved), _p(ws)))
         return out, aux, z, saved
 
+    def forward_noalloc(self, x2d, wstruct, out, aux, z):
+        """Forward-only call into caller-allocated outputs through
+        moe_forward_noalloc: the library's static scratch, no workspace."""
+        _lib.check(_lib.load().moe_forward_noalloc(self.h, self._stream(), x2d.shape[0], _p(x2d),
+                                                   ctypes.byref(wstruct), _p(out), _p(aux),
+                                                   _p(z)))
+        return out, aux, z
+
     def backward(self, x2d, dout, wstruct, gstruct, saved, dx=None, d_aux=None, d_z=None,
                  has_grad=None):
         T = x2d.shape[0]
