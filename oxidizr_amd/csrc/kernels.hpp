@@ -163,6 +163,9 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
 // gradients: faster for the dense ones (shared expert: 1-3 %) and for groups
 // of >= 512 rows (configs 2 and 3: step -1.1 % / -0.4 %), slower for
 // config 5's ~256-row groups (gate/up pair +5 %).
+// xcd_order (grouped, G a multiple of 8): when not null and its flag
+// xcd_order[G] is set, XCD x runs the whole groups xcd_order[x * G / 8 + j],
+// j < G / 8 (k_xcd_order), one after another, instead of 1/8 of every group.
 struct KGroups {
   const int* offsets;
   int G;
@@ -170,6 +173,7 @@ struct KGroups {
   int nsplit;
   int kchunk;
   int col_walk;
+  const int* xcd_order;
 };
 
 MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& split,
@@ -181,10 +185,21 @@ MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp,
   // differ widely, and whole groups per XCD would leave the XCD that holds the
   // busiest expert running long after the others.
   const int per = nM * nN;
-  const int span = 8 * ((per + 7) >> 3);
-  const int gs = uni(blockIdx.x / span);   // group (grouped) or split chunk (dense)
-  int r;
-  if (!xcd_slot(blockIdx.x - gs * span, per, r)) return false;
+  int gs, r;  // group (grouped) or split chunk (dense); tile of it
+  if (g.xcd_order && g.xcd_order[g.G]) {
+    // whole groups per XCD: block b runs on XCD b % 8 and is that XCD's
+    // (b / 8)-th block; the grid of 8 * ceil(per / 8) blocks per group covers
+    // G / 8 groups of per tiles on every XCD
+    const int epx = g.G >> 3, local = (int)(blockIdx.x >> 3);
+    const int j = uni(local / per);
+    if (j >= epx) return false;
+    r = uni(local - j * per);
+    gs = uni(g.xcd_order[(int)(blockIdx.x & 7) * epx + j]);
+  } else {
+    const int span = 8 * ((per + 7) >> 3);
+    gs = uni(blockIdx.x / span);
+    if (!xcd_slot(blockIdx.x - gs * span, per, r)) return false;
+  }
   if (g.col_walk) {
     int mt, nt;
     if (!tile_order(r, nM, nN, mt, nt)) return false;
@@ -208,6 +223,47 @@ MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp,
     K = min(g.kchunk, g.K - krow0);
   }
   return K > 0;
+}
+
+// Expert order of a grouped weight gradient over the 8 XCDs (E a multiple of
+// 8, one block of 1024 threads): the experts ranked by token count (most
+// first, ties by index) are dealt in a snake, rank r to XCD r % 8 in even
+// rounds r / 8 and to 7 - r % 8 in odd ones, so every XCD holds E / 8 whole
+// experts: each XCD's L2 then reads an expert's operand panels once instead of
+// all eight reading every expert (config 5 gate/up weight gradient: 7.7 ->
+// 6.7 ms; for the down projection's weight gradient, whose larger operand is
+// already split over the XCDs, it measured slower).  order[E] = 1 when the
+// busiest XCD holds at most 8 % more rows than the mean, else 0 (the kernels
+// then deal every expert's tiles over all XCDs).  Integer arithmetic only.
+__global__ __launch_bounds__(1024) void k_xcd_order(const int* __restrict__ counts, int E,
+                                                    int* __restrict__ order) {
+  __shared__ int cnt[1024];
+  __shared__ int load[8];
+  const int tid = threadIdx.x;
+  for (int e = tid; e < E; e += 1024) cnt[e] = counts[e];
+  if (tid < 8) load[tid] = 0;
+  __syncthreads();
+  for (int e = tid; e < E; e += 1024) {
+    const int c = cnt[e];
+    int rank = 0;
+    for (int f = 0; f < E; ++f) {
+      const int d = cnt[f];
+      rank += (d > c || (d == c && f < e)) ? 1 : 0;
+    }
+    const int round = rank >> 3, pos = rank & 7, x = (round & 1) ? 7 - pos : pos;
+    order[x * (E >> 3) + round] = e;
+    atomicAdd(&load[x], c);
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int64_t total = 0;
+    int mx = 0;
+    for (int x = 0; x < 8; ++x) {
+      total += load[x];
+      mx = max(mx, load[x]);
+    }
+    order[E] = 100 * 8 * (int64_t)mx <= 108 * total ? 1 : 0;
+  }
 }
 
 template <typename T>

@@ -70,7 +70,7 @@ struct WsLayout {
   size_t block_hist, block_base, colpart, ghist, gbase, gpart, sY, infer;
   // backward
   size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
-      recomp, dxm, dwn, dwn_a, dwn_b;
+      recomp, dxm, dwn, dwn_a, dwn_b, xorder;
   size_t total;
   size_t fwd_total;  // bytes a forward-only call touches (the forward regions)
 };
@@ -294,6 +294,8 @@ struct moe_plan {
     L.dwn = g.take(blk ? 4 * (size_t)nrow * H : 0);
     L.dwn_a = g.take(blk ? 4 * (size_t)ceil_div(nrow, 16) * H : 0);
     L.dwn_b = g.take(blk ? 4 * (size_t)ceil_div(nrow, 256) * H : 0);
+    // expert order of the gate/up weight gradient over the 8 XCDs and its flag
+    L.xorder = g.take(4 * (size_t)(E + 1));
     L.total = f.off > g.off ? f.off : g.off;
     L.fwd_total = f.off;
     return L;
@@ -539,7 +541,7 @@ void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, co
   using C = typename std::conditional<NA == 2, typename Tilings<D>::WgradPair,
                                       typename Tilings<D>::Big>::type;
   const SplitPlan sp = plan_split<C>(M, N, T);
-  const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk, 1};
+  const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk, 1, nullptr};
   hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN)),
                      dim3(256), 0, s, P0, P1, ldp, Q,
                      ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
@@ -867,7 +869,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   D* const* tdg = (D* const*)(p->d_tab + 3 * E);
   D* const* tdu = (D* const*)(p->d_tab + 4 * E);
   D* const* tdd = (D* const*)(p->d_tab + 5 * E);
-  const KGroups kg{offsets, E, 0, 1, 0, TK >= 512 * (int64_t)E ? 1 : 0};
+  const KGroups kg{offsets, E, 0, 1, 0, TK >= 512 * (int64_t)E ? 1 : 0, nullptr};
   float* partial = (float*)(ws + W.splitk_router);
   // Shared expert backward first, on the plan's second stream: it needs only
   // d_out, x and its own saved activations.  Its input gradient comes first
@@ -923,6 +925,13 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   // gradient, dG / dU); the input gradients and the router backward on s.
   const hipStream_t ws2 = p->wgrad_stream(s);
   HIP_TRY(wgrad_join.fork(s, ws2, p->wfork, p->wjoin));
+  // whole experts per XCD for the gate/up weight gradient when the experts
+  // split evenly over the XCDs (k_xcd_order decides on the device)
+  int* xorder = E % 8 == 0 ? (int*)(ws + W.xorder) : nullptr;
+  if (xorder) {
+    hipLaunchKernelGGL(k_xcd_order, dim3(1), dim3(1024), 0, ws2, counts, E, xorder);
+    LAUNCH_CHECK();
+  }
   {
     StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
     const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
@@ -946,8 +955,10 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   {
     StageTimer tm(p, ws2, MOE_STAGE_GATEUP_WGRAD);
     const int grid = kgrouped_grid(E, I, H, CW::BM, CW::BN);
+    KGroups kgp = kg;
+    kgp.xcd_order = xorder;
     hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(256), 0, ws2, dG, dU, (int64_t)I, xp,
-                       (int64_t)H, kg, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
+                       (int64_t)H, kgp, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
   {
