@@ -1,7 +1,7 @@
 // Tiled MFMA GEMM main loop for the MoE layer (gfx950 / CDNA4).
 //
-// One workgroup = 256 threads = 4 wave64s in a 2 x 2 arrangement computes a
-// BM x BN output tile of  C[m, n] = sum_k A(m, k) * B(n, k).
+// One workgroup of 4 or 8 wave64s (Tiling::NW) in a WGM x WGN arrangement
+// computes a BM x BN output tile of  C[m, n] = sum_k A(m, k) * B(n, k).
 // Operands are staged through LDS as K-contiguous rows ([row][k], padded by
 // one 16-byte vector per row against bank conflicts). An operand whose memory
 // layout is K-major ("transposed": element (r, k) at base + k * ld + r) is
@@ -23,19 +23,20 @@
 
 namespace moe {
 
-// BM x BN output tile per workgroup of 4 waves arranged WGM x WGN (wave w
+// BM x BN output tile per workgroup of NW waves arranged WGM x WGN (wave w
 // owns block (w / WGN, w % WGN)), BK-deep k-tiles.
-template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2, int NST_ = 2>
+template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2, int NST_ = 2, int NW_ = 4>
 struct Tiling {
   static constexpr int BM = BM_, BN = BN_, BK = BK_;
   static constexpr int NST = NST_;        // LDS pipeline stages (direct-to-LDS loop)
   static constexpr int V = Vec16<T>::N;   // elements per 16-byte vector
   static constexpr int LDK = BK + V;      // padded LDS row pitch (elements)
-  static constexpr int THREADS = 256;
-  static constexpr int WGN = WGN_, WGM = 4 / WGN_;  // wave grid
+  static constexpr int NW = NW_;          // waves per workgroup
+  static constexpr int THREADS = 64 * NW;
+  static constexpr int WGN = WGN_, WGM = NW_ / WGN_;  // wave grid
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // per-wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA blocks per wave
-  static_assert(WGM * WGN == 4, "four waves");
+  static_assert(WGM * WGN == NW && (NW == 4 || NW == 8), "four or eight waves");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tiles of whole 32 x 32 blocks");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % (2 * V) == 0, "BK must cover whole MFMA k-steps");
@@ -229,8 +230,8 @@ struct DmaStager {
   static constexpr int KV = C::BK / C::V;    // 16-byte slots per row
   static_assert(KV == 8 || KV == 4, "rows of 8 or 4 slots");
   static constexpr int RPI = 64 / KV;        // rows per wave per 1 KB instruction
-  static_assert(R % (4 * RPI) == 0, "4 waves x RPI rows per instruction");
-  static constexpr int PER = R / (4 * RPI);  // instructions per wave per k-tile
+  static_assert(R % (C::NW * RPI) == 0, "NW waves x RPI rows per instruction");
+  static constexpr int PER = R / (C::NW * RPI);  // instructions per wave per k-tile
   // slot swizzle: the 16 lanes of a ds_read_b128 phase read 16 rows at one kv
   // and must hit 16 distinct 16-byte bank groups of a 256-byte window
   MOE_DEV static int swz(int r) { return KV == 8 ? nt_swz(r) : ((r >> 2) & 3); }
@@ -249,7 +250,7 @@ struct DmaStager {
     const int row = wave * RPI + lane / KV;   // the swizzle bits are the same for every chunk i
     kcol = ((lane % KV) ^ swz(row)) * C::V;
     voff = (uint32_t)((row * d.ld + kcol) * (int64_t)sizeof(T));
-    step = (uint32_t)(4 * RPI * d.ld * (int64_t)sizeof(T));
+    step = (uint32_t)(C::NW * RPI * d.ld * (int64_t)sizeof(T));
   }
   MOE_DEV void init_second(const OpDesc<T>& d) {  // same ld and rows as the first
     rs[1] = rsrc_of(d);
@@ -263,7 +264,7 @@ struct DmaStager {
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs[seg], (lds_void_t*)(tile + (i * 4 * RPI + wave * RPI) * C::BK), 16,
+          rs[seg], (lds_void_t*)(tile + (i * C::NW * RPI + wave * RPI) * C::BK), 16,
           kin ? voff + i * step : kOobOffset, soff, 0, 0);
   }
   MOE_DEV static u32x4 frag(const T* tile, int row, int kv) {
@@ -276,8 +277,8 @@ struct DmaStagerT {
   static_assert(sizeof(T) == 2, "transposing LDS reads are 16-bit");
   static constexpr int SPR = R / 8;              // 16-byte slots per k-row
   static constexpr int RPI = 64 / SPR;           // k-rows per 1 KB instruction
-  static constexpr int PER = C::BK / (4 * RPI);  // instructions per wave per k-tile
-  static_assert(PER >= 1 && C::BK % (4 * RPI) == 0, "k-rows must cover the waves");
+  static constexpr int PER = C::BK / (C::NW * RPI);  // instructions per wave per k-tile
+  static_assert(PER >= 1 && C::BK % (C::NW * RPI) == 0, "k-rows must cover the waves");
   rsrc_t rs[2];
   uint32_t voff, ldb;
   MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
@@ -300,8 +301,8 @@ struct DmaStagerT {
 #pragma unroll
     for (int i = 0; i < PER; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          rs[seg], (lds_void_t*)(tile + (i * 4 * RPI + wave * RPI) * R), 16,
-          voff + (uint32_t)(i * 4 * RPI) * ldb, (uint32_t)k0 * ldb, 0, 0);
+          rs[seg], (lds_void_t*)(tile + (i * C::NW * RPI + wave * RPI) * R), 16,
+          voff + (uint32_t)(i * C::NW * RPI) * ldb, (uint32_t)k0 * ldb, 0, 0);
   }
   // operand of the fragment whose first column is col0, k-step starting at kk
   MOE_DEV static u32x4 frag(const T* tile, int col0, int kk) {
@@ -653,7 +654,8 @@ MOE_DEV void for_each_frag(const f32x16 (&acc)[NACC][C::TN][C::TM], F&& f) {
 // LDS floats the row epilogue needs: every wave stages NACC blocks of WM x 32
 // accumulators, rows padded to 36 floats.
 template <class C, int NACC>
-constexpr int epi_lds_floats() { return 4 * NACC * C::WM * 36; }
+constexpr int epi_lds_floats() { return C::NW * NACC * C::WM * 36; }
+constexpr int kLdsBytes = 160 * 1024;  // LDS one workgroup may hold on gfx950
 
 // LDS elements of a kernel whose main loop (NA A / NB B operands) is followed
 // by the row epilogue over NACC accumulator sets in the same buffer.
@@ -747,7 +749,7 @@ MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, 
 // for_each_row8.
 constexpr int kRowPitchBf16 = 40;
 template <class C, int NACC>
-constexpr int epi_lds_bf16_elems() { return 4 * NACC * C::WM * kRowPitchBf16; }
+constexpr int epi_lds_bf16_elems() { return C::NW * NACC * C::WM * kRowPitchBf16; }
 template <class C, int NACC, class F>
 MOE_DEV void for_each_row8_bf16(const f32x16 (&acc)[NACC][C::TN][C::TM], bf16_t* lds, float scale,
                                 F&& f) {

@@ -18,18 +18,24 @@
 namespace moe {
 
 // ------------------------------------------------------------------ tilings
-// One tiling per GEMM role.  bf16 tiles are 256 wide where the operands allow
-// it: a 2 x 2 wave grid then gives every wave a 128 x 128 accumulator block
-// (256 accumulator registers), which halves the LDS bytes read per MFMA
-// against 64 x 64 wave blocks.  The gate/up forward (two B operands) and the
-// paired wgrad (two A operands) halve the other side to keep 256 accumulators.
-// Router-sized GEMMs (one side = E) keep 128 x 128.  fp32 keeps 128 x 128.
+// One tiling per GEMM role.  bf16 tiles are 256 x 256 outputs per workgroup
+// (the gate/up forward's two B operands and the paired wgrad's two A
+// operands each halve one side), one workgroup per CU.  The expert GEMMs run
+// eight waves per workgroup, two per SIMD, each with a 64 x 128 (or 64 x 64
+// per operand pair) block in 128 accumulation registers: while one wave of a
+// SIMD waits on the k-tile's DMA or barrier the other issues MFMAs, and eight
+// waves keep more direct-to-LDS loads in flight (a microbenchmark of the
+// k-tile pattern: 1.92 -> 1.59 us per k-tile against four waves).  Measured
+// against four waves with 128 x 128 blocks: config 5 step 30.2 -> 29.2 ms,
+// config 2 2.13 -> 2.02 ms, config 3 8.33 -> 7.94 ms (same bits: each output
+// keeps its k order).  Router-sized GEMMs (one side = E) keep 128 x 128 and
+// four waves.  fp32 keeps four waves.
 template <typename T> struct Tilings;
 template <> struct Tilings<bf16_t> {
   using Router = Tiling<bf16_t, 128, 128, 64>;
-  using GateUp = Tiling<bf16_t, 256, 128, 64>;
-  using Big = Tiling<bf16_t, 256, 256, 64>;
-  using WgradPair = Tiling<bf16_t, 128, 256, 64>;
+  using GateUp = Tiling<bf16_t, 256, 128, 64, 2, 2, 8>;
+  using Big = Tiling<bf16_t, 256, 256, 64, 2, 2, 8>;
+  using WgradPair = Tiling<bf16_t, 128, 256, 64, 4, 2, 8>;
 };
 // fp32 (config 1: T = 1024, H = 384, I = 1024): 64-column tiles give the
 // N = H GEMMs 96 workgroups instead of the 48 that 128-column tiles leave for
@@ -893,20 +899,28 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // 79 % useful rows with BM/2 granularity and 94 % with BM/4.  Every output
 // element keeps its k order (same bits).  bf16 256-row tiles only.
 template <class C>
-using QuarterRows = Tiling<bf16_t, C::BM / 4, C::BN, C::BK, 4, C::NST>;
+using QuarterRows = Tiling<bf16_t, C::BM / 4, C::BN, C::BK, 4, C::NST, C::NW>;
 template <class C>
-using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4, C::NST>;
+using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4, C::NST, C::NW>;
 template <class C>
-using ThreeQuarterRows = Tiling<bf16_t, 3 * C::BM / 4, C::BN, C::BK, 2, C::NST>;
+using ThreeQuarterRows = Tiling<bf16_t, 3 * C::BM / 4, C::BN, C::BK, C::NW / 2, C::NST, C::NW>;
 template <typename T, class C>
 constexpr bool has_half_rows() { return sizeof(T) == 2 && C::BM == 256; }
+// The 3BM/4-row tiling's wave blocks are 96 rows tall; with eight waves and
+// two accumulator sets its epilogue staging would outgrow the LDS, and such
+// tails then run as full tiles.
+template <class C, int NACC>
+constexpr bool has_three_quarter_rows() {
+  return epi_lds_floats<ThreeQuarterRows<C>, NACC>() * 4 <= kLdsBytes;
+}
 template <typename T, class C, int NA, int NB, int NACC>
 constexpr int rowgroup_smem_elems() {
   constexpr int a = kernel_smem_elems<C, T, NA, NB, NACC>();
   if constexpr (has_half_rows<T, C>()) {
     constexpr int b = kernel_smem_elems<QuarterRows<C>, T, NA, NB, NACC>();
     constexpr int c = kernel_smem_elems<HalfRows<C>, T, NA, NB, NACC>();
-    constexpr int d = kernel_smem_elems<ThreeQuarterRows<C>, T, NA, NB, NACC>();
+    constexpr int d = has_three_quarter_rows<C, NACC>()
+                          ? kernel_smem_elems<ThreeQuarterRows<C>, T, NA, NB, NACC>() : 0;
     constexpr int ab = a > b ? a : b, cd = c > d ? c : d;
     return ab > cd ? ab : cd;
   } else {
@@ -914,8 +928,8 @@ constexpr int rowgroup_smem_elems() {
   }
 }
 // Runs body(tiling) for a resolved row tile with mv valid rows: the shortest
-// row tiling that covers them.
-template <typename T, class C, class F>
+// row tiling that covers them (NACC: the kernel's accumulator sets).
+template <typename T, class C, int NACC, class F>
 MOE_DEV void with_tile_rows(int mv, F&& body) {
   if constexpr (has_half_rows<T, C>()) {
     if (mv <= C::BM / 4) {
@@ -926,9 +940,11 @@ MOE_DEV void with_tile_rows(int mv, F&& body) {
       body(HalfRows<C>{});
       return;
     }
-    if (mv <= 3 * C::BM / 4) {
-      body(ThreeQuarterRows<C>{});
-      return;
+    if constexpr (has_three_quarter_rows<C, NACC>()) {
+      if (mv <= 3 * C::BM / 4) {
+        body(ThreeQuarterRows<C>{});
+        return;
+      }
     }
   }
   body(C{});
@@ -938,7 +954,7 @@ MOE_DEV void with_tile_rows(int mv, F&& body) {
 // 128-column tile with the four waves stacked along M (HalfCols<C>), with the
 // same per-element k order (same bits).  bf16 256-column tiles only.
 template <class C>
-using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, 1, C::NST>;
+using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, C::NW / 4, C::NST, C::NW>;
 template <typename T, class C>
 constexpr bool has_half_cols() { return sizeof(T) == 2 && C::BN == 256; }
 template <typename T, class C, int NA, int NB, int NACC>
@@ -973,16 +989,18 @@ MOE_DEV void with_tile_shape(int mv, int nv, F&& body) {
     }
   }
   if constexpr (has_half_rows<T, C>()) {
-    if (mv <= 3 * C::BM / 4) {
-      body(ThreeQuarterRows<C>{});
-      return;
+    if constexpr (has_three_quarter_rows<C, 1>()) {
+      if (mv <= 3 * C::BM / 4) {
+        body(ThreeQuarterRows<C>{});
+        return;
+      }
     }
   }
   body(C{});
 }
 
 template <typename T, bool GROUPED, class C = typename Tilings<T>::GateUp>
-__global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
+__global__ __launch_bounds__(C::THREADS) void k_gateup_fwd(const T* __restrict__ X, RowGroups groups,
                                                     const T* const* wg_tab, const T* wg_one,
                                                     const T* const* wu_tab, const T* wu_one,
                                                     int H, int N, T* __restrict__ G,
@@ -992,7 +1010,7 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
   if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);
   const T* wu = pick(wu_tab, wu_one, grp);
-  with_tile_rows<T, C>(mv, [&](auto ct) {
+  with_tile_rows<T, C, 2>(mv, [&](auto ct) {
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{X + (int64_t)row0 * H, H, mv, H}};
     OpDesc<T> b[2] = {{wg + (int64_t)n0 * H, H, N - n0, H}, {wu + (int64_t)n0 * H, H, N - n0, H}};
@@ -1017,14 +1035,14 @@ __global__ __launch_bounds__(256) void k_gateup_fwd(const T* __restrict__ X, Row
 
 // Y = A Wd^T per row group (K = I) or for the dense shared expert.
 template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
-__global__ __launch_bounds__(256) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
+__global__ __launch_bounds__(C::THREADS) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
                                                   const T* const* wd_tab, const T* wd_one, int I,
                                                   int H, T* __restrict__ Y) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);
-  with_tile_rows<T, C>(mv, [&](auto ct) {
+  with_tile_rows<T, C, 1>(mv, [&](auto ct) {
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{A + (int64_t)row0 * I, I, mv, I}};
     OpDesc<T> b[1] = {{wd + (int64_t)n0 * I, I, H - n0, I}};
@@ -1145,7 +1163,7 @@ __global__ __launch_bounds__(256) void k_combine_bwd(const T* __restrict__ dout,
 // dA = alpha * dY Wd (NN, K = H), then the SwiGLU backward in the epilogue:
 // dG = dA * U * silu'(G), dU = dA * silu(G).
 template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
-__global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, RowGroups groups,
+__global__ __launch_bounds__(C::THREADS) void k_down_dgrad(const T* __restrict__ dY, RowGroups groups,
                                                     const T* const* wd_tab, const T* wd_one,
                                                     int H, int N, float alpha,
                                                     const T* __restrict__ G,
@@ -1205,7 +1223,7 @@ __global__ __launch_bounds__(256) void k_down_dgrad(const T* __restrict__ dY, Ro
 
 // dX = dG Wg + dU Wu (NN, K = I twice) per row group.
 template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
-__global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
+__global__ __launch_bounds__(C::THREADS) void k_gateup_dgrad(const T* __restrict__ dG,
                                                       const T* __restrict__ dU, RowGroups groups,
                                                       const T* const* wg_tab, const T* wg_one,
                                                       const T* const* wu_tab, const T* wu_one,
@@ -1215,7 +1233,7 @@ __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
   if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);  // [I, H]: element (n=h, k=i) at wg + i*H + h
   const T* wu = pick(wu_tab, wu_one, grp);
-  with_tile_rows<T, C>(mv, [&](auto ct) {
+  with_tile_rows<T, C, 1>(mv, [&](auto ct) {
     using CT = decltype(ct);
     f32x16 acc[1][CT::TN][CT::TM];
     zero_acc<CT, 1>(acc);
@@ -1237,14 +1255,17 @@ __global__ __launch_bounds__(256) void k_gateup_dgrad(const T* __restrict__ dG,
 //   W_a[g][m, n] = alpha * sum_r P_a[r, m] * Q[r, n],  r over the group's rows,
 // with NA = 1 (single) or 2 (two P operands sharing Q).  P is [rows, M]
 // (ld = ldp), Q is [rows, N] (ld = ldq), outputs [M, N].
+template <typename T, int NA>
+using WgradTiling = typename std::conditional<NA == 2, typename Tilings<T>::WgradPair,
+                                              typename Tilings<T>::Big>::type;
 template <typename T, int NA, bool GROUPED>
-__global__ __launch_bounds__(256) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
+__global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
                                                int64_t ldp, const T* __restrict__ Q, int64_t ldq,
                                                KGroups groups, int M, int N, float alpha,
                                                T* const* out0_tab, T* out0_one,
                                                T* const* out1_tab, T* out1_one,
                                                float* __restrict__ partial) {
-  using C = typename std::conditional<NA == 2, typename Tilings<T>::WgradPair, typename Tilings<T>::Big>::type;
+  using C = WgradTiling<T, NA>;
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, NA, 1, NA>()];
   int grp, split, krow0, K, m0, n0;
   if (!resolve_k(groups, M, N, C::BM, C::BN, grp, split, krow0, K, m0, n0)) return;

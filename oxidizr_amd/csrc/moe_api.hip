@@ -538,12 +538,11 @@ template <typename D, int NA>
 void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, const D* Q,
                         int64_t ldq, int T, int M, int N, float alpha, D* o0, D* o1,
                         float* partial) {
-  using C = typename std::conditional<NA == 2, typename Tilings<D>::WgradPair,
-                                      typename Tilings<D>::Big>::type;
+  using C = WgradTiling<D, NA>;
   const SplitPlan sp = plan_split<C>(M, N, T);
   const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk, 1, nullptr};
   hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN)),
-                     dim3(256), 0, s, P0, P1, ldp, Q,
+                     dim3(C::THREADS), 0, s, P0, P1, ldp, Q,
                      ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
   if (sp.nsplit > 1) {
     const int64_t MN = (int64_t)M * N;
@@ -617,11 +616,11 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   } else {
     const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
     hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
-                       dim3(256), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                       dim3(CG::THREADS), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, H, S, sG, sU, sA);
     if (sY)
       hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
-                         dim3(256), 0, ss, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+                         dim3(CB::THREADS), 0, ss, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
   }
 }
 
@@ -692,7 +691,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
     } else {
       with_row_tiling<D, CG>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
         using C = decltype(c);
-        hipLaunchKernelGGL((k_gateup_fwd<D, true, C>), dim3(grid(I)), dim3(256), 0,
+        hipLaunchKernelGGL((k_gateup_fwd<D, true, C>), dim3(grid(I)), dim3(C::THREADS), 0,
                            s, st.xp, r, tg, nullptr, tu, nullptr, H, I, st.G, st.U, st.A);
       });
     }
@@ -711,7 +710,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
     } else {
       with_row_tiling<D, CB>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
         using C = decltype(c);
-        hipLaunchKernelGGL((k_down_fwd<D, true, C>), dim3(grid(H)), dim3(256), 0, s,
+        hipLaunchKernelGGL((k_down_fwd<D, true, C>), dim3(grid(H)), dim3(C::THREADS), 0, s,
                            st.A, r, td, nullptr, I, H, st.Y);
       });
     }
@@ -896,9 +895,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     dxs = (D*)(ws + W.dxs);
     const float sc = c.shared_expert_scale;
     const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
-    hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(256), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
+    hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(CB::THREADS), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
-    hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(256), 0, ss, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
+    hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(CB::THREADS), 0, ss, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, S, H, dxs);
     if (ss != s) {
       HIP_TRY(hipEventRecord(p->sdx, ss));
@@ -935,7 +934,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   {
     StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
     const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
-    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(256), 0, ws2, dY, nullptr, (int64_t)H, A,
+    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(CB::THREADS), 0, ws2, dY, nullptr, (int64_t)H, A,
                        (int64_t)I, kg, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
   }
@@ -943,7 +942,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     StageTimer tm(p, s, MOE_STAGE_DOWN_DGRAD);
     with_row_tiling<D, CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
-      hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(grid(I)), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(grid(I)), dim3(C::THREADS), 0, s,
                          dY, r, td, nullptr, H, I, 1.0f, G, U, dG, dU);
     });
     LAUNCH_CHECK();
@@ -957,7 +956,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     const int grid = kgrouped_grid(E, I, H, CW::BM, CW::BN);
     KGroups kgp = kg;
     kgp.xcd_order = xorder;
-    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(256), 0, ws2, dG, dU, (int64_t)I, xp,
+    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(CW::THREADS), 0, ws2, dG, dU, (int64_t)I, xp,
                        (int64_t)H, kgp, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
     LAUNCH_CHECK();
   }
@@ -965,7 +964,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     StageTimer tm(p, s, MOE_STAGE_GATEUP_DGRAD);
     with_row_tiling<D, CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
-      hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(grid(H)), dim3(256), 0,
+      hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(grid(H)), dim3(C::THREADS), 0,
                          s, dG, dU, r, tg, nullptr, tu, nullptr, I, H, dXp);
     });
     LAUNCH_CHECK();
