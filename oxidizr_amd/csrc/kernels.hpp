@@ -28,14 +28,17 @@ namespace moe {
 // k-tile pattern: 1.92 -> 1.59 us per k-tile against four waves).  Measured
 // against four waves with 128 x 128 blocks: config 5 step 30.2 -> 29.2 ms,
 // config 2 2.13 -> 2.02 ms, config 3 8.33 -> 7.94 ms (same bits: each output
-// keeps its k order).  Router-sized GEMMs (one side = E) keep 128 x 128 and
-// four waves.  fp32 keeps four waves.
+// keeps its k order).  The paired weight gradient's waves are stacked 4 x 2
+// (32 x 128 blocks per operand): config 5's gate/up weight gradient 6.79 ->
+// 6.61 ms against 2 x 4; a 2 x 4 grid for the 256 x 256 tiles made the down
+// weight gradient 14 % slower.  Router-sized GEMMs (one side = E) keep
+// 128 x 128 and four waves.  fp32 keeps four waves.
 template <typename T> struct Tilings;
 template <> struct Tilings<bf16_t> {
   using Router = Tiling<bf16_t, 128, 128, 64>;
   using GateUp = Tiling<bf16_t, 256, 128, 64, 2, 2, 8>;
   using Big = Tiling<bf16_t, 256, 256, 64, 2, 2, 8>;
-  using WgradPair = Tiling<bf16_t, 128, 256, 64, 4, 2, 8>;
+  using WgradPair = Tiling<bf16_t, 128, 256, 64, 2, 2, 8>;
 };
 // fp32 (config 1: T = 1024, H = 384, I = 1024): 64-column tiles give the
 // N = H GEMMs 96 workgroups instead of the 48 that 128-column tiles leave for
