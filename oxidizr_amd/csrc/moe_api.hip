@@ -596,12 +596,12 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   const int H = p->cfg.hidden, S = p->cfg.shared_intermediate;
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   if (skinny && T <= 16) {
-    hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, kSkinnyRows)), dim3(256), 0, ss,
+    hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(ceil_div(S, kSkinnyRows)), dim3(256), kSkinnyLdsReserve, ss,
                        (const bf16_t*)x, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_gate,
                        nullptr, (const bf16_t*)w->shared_up, H, S, (bf16_t*)sG, (bf16_t*)sU,
                        (bf16_t*)sA);
     if (sY)
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, kSkinnyRows)), dim3(256), 0, ss,
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(ceil_div(H, kSkinnyRows)), dim3(256), kSkinnyLdsReserve, ss,
                          (const bf16_t*)sA, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else if (skinny) {
@@ -679,7 +679,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   {
     StageTimer tm(p, s, stage(MOE_STAGE_GATEUP_FWD));
     if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, kSkinnyRows)), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_skinny_fwd<true, false>), dim3(E * ceil_div(I, kSkinnyRows)), dim3(256), kSkinnyLdsReserve, s,
                          xsrc, xrow, k, T, st.offsets, E, 0, (const bf16_t* const*)tg, nullptr,
                          (const bf16_t* const*)tu, nullptr, H, I, (bf16_t*)st.G, (bf16_t*)st.U,
                          (bf16_t*)st.A);
@@ -700,7 +700,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   {
     StageTimer tm(p, s, stage(MOE_STAGE_DOWN_FWD));
     if (skinny) {
-      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, kSkinnyRows)), dim3(256), 0, s,
+      hipLaunchKernelGGL((k_skinny_fwd<false, false>), dim3(E * ceil_div(H, kSkinnyRows)), dim3(256), kSkinnyLdsReserve, s,
                          (const bf16_t*)st.A, nullptr, 1, 0, st.offsets, E, 0, (const bf16_t* const*)td, nullptr,
                          nullptr, nullptr, I, H, (bf16_t*)st.Y, nullptr, nullptr);
       if (T > 16)
