@@ -318,13 +318,15 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
 // `row` holds the token's E logits (global memory, or a row staged in LDS by
 // the fused router kernel): the same arithmetic either way, so the same bits.
 // Also returns, in registers, the lane's probabilities pr[i] (expert
-// lane + 64 i, 0 past E) and the chosen experts sel[0..k) (the same in every
-// lane).
+// lane + 64 i, 0 past E) and, in lane j < k, the j-th chosen expert (sel;
+// -1 in lanes >= k).  Selection j is kept by lane j rather than in arrays
+// indexed by the runtime k, which the compiler would keep in scratch or in
+// 48 extra registers.
 template <int EPL>
 MOE_DEV void route_row(const float* row, int t, int E, int k, float tau,
                        int norm, float* __restrict__ probs, float* __restrict__ lse,
                        int* __restrict__ idx, float* __restrict__ w, float (&pr)[EPL],
-                       int (&sel)[16]) {
+                       int& sel) {
   const int lane = threadIdx.x & 63;
   float v[EPL], ex[EPL];
   float mx = -INFINITY;
@@ -352,8 +354,8 @@ MOE_DEV void route_row(const float* row, int t, int E, int k, float tau,
   if (lane == 0) lse[t] = mx + logf(s);
 
   uint32_t taken = 0;
-  float wsel[16];
-  int isel[16];
+  float wsel = 0.0f;
+  sel = -1;
   float wsum = 0.0f;
   for (int j = 0; j < k; ++j) {
     float bv = -INFINITY;
@@ -386,16 +388,15 @@ MOE_DEV void route_row(const float* row, int t, int E, int k, float tau,
         mine = ex[i];
       }
     const float pj = __shfl(mine, be & 63, 64) / s;
-    wsel[j] = pj;
-    isel[j] = be;
-    sel[j] = be;
+    if (lane == j) {
+      wsel = pj;
+      sel = be;
+    }
     wsum += pj;
   }
-  if (lane == 0) {
-    for (int j = 0; j < k; ++j) {
-      idx[(int64_t)t * k + j] = isel[j];
-      w[(int64_t)t * k + j] = norm ? wsel[j] / wsum : wsel[j];
-    }
+  if (lane < k) {
+    idx[(int64_t)t * k + lane] = sel;
+    w[(int64_t)t * k + lane] = norm ? wsel / wsum : wsel;
   }
 }
 
@@ -408,27 +409,32 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
   float pr[EPL];
-  int sel[16];
+  int sel;
   route_row<EPL>(logits + (int64_t)t * E, t, E, k, tau, norm, probs, lse, idx, w, pr, sel);
 }
 
 // ------------------------------------------------------------------ fused router
 // Router GEMM, softmax, log-sum-exp and top-k in one launch (bf16, up to
 // kFusedRouterMaxExperts experts).  A workgroup of kRouterWaves waves owns 16
-// tokens and every expert (NEB = ceil(E / 16) blocks of 16): as in
-// k_router_small each wave takes every kRouterWaves-th 256-wide k-chunk of the
-// hidden dimension and multiplies its 16 token rows with the NEB router-row
-// blocks (v_mfma_f32_16x16x32_bf16), the partial sums are added through LDS in
-// wave order, and each of the 16 waves then routes one token with route_row
-// (the arithmetic of k_route) from the logits row staged in LDS.
+// tokens and every expert (NEB = ceil(E / 16) blocks of 16): each wave takes
+// every kRouterWaves-th kFusedRouterChunk-wide k-chunk of the hidden dimension
+// and multiplies its 16 token rows with the NEB router-row blocks
+// (v_mfma_f32_16x16x32_bf16), the partial sums are added through LDS in wave
+// order, and each of the 16 waves then routes one token with route_row (the
+// arithmetic of k_route) from the logits row staged in LDS.  128-wide chunks
+// give every wave a chunk at H = 2048 and keep the loads in flight within
+// 64 VGPRs, so two workgroups share a CU (256-wide chunks: half the waves
+// idle at H = 2048, 72 VGPRs, one workgroup per CU, two rounds of
+// workgroups for 8192 tokens).
 constexpr int kFusedRouterMaxExperts = 64;
+constexpr int kFusedRouterChunk = 128;
 // The workgroup also writes what the dispatch and the losses need from its 16
 // tokens: the expert histogram of their k choices (group_hist[b][e], an
 // integer LDS histogram) and the column sums of their probabilities
 // (prob_part[b][e], tokens added in order), so that k_scan over the 16-token
 // groups and k_colsum_final finish the counts, offsets and P.
 template <int NEB>
-__global__ __launch_bounds__(64 * kRouterWaves) void k_router_route(
+__global__ __launch_bounds__(64 * kRouterWaves) __attribute__((amdgpu_waves_per_eu(8))) void k_router_route(
     const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, const float* __restrict__ bias,
     int Tn, int H, int E, int k, float tau, int norm, float* __restrict__ logits,
     float* __restrict__ probs, float* __restrict__ lse, int* __restrict__ idx,
@@ -448,12 +454,13 @@ __global__ __launch_bounds__(64 * kRouterWaves) void k_router_route(
   f32x4 acc[NEB];
 #pragma unroll
   for (int b = 0; b < NEB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int kc = wave; kc * 256 < H; kc += kRouterWaves) {
-    const uint32_t soff = (uint32_t)kc * 512;
-    u32x4 xa[8], wa[NEB][8];
+  for (int kc = wave; kc * kFusedRouterChunk < H; kc += kRouterWaves) {
+    constexpr int NQ = kFusedRouterChunk / 32;
+    const uint32_t soff = (uint32_t)kc * (2 * kFusedRouterChunk);
+    u32x4 xa[NQ], wa[NEB][NQ];
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const bool kin = kc * 256 + 32 * q + 8 * g < H;
+    for (int q = 0; q < NQ; ++q) {
+      const bool kin = kc * kFusedRouterChunk + 32 * q + 8 * g < H;
       xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
 #pragma unroll
       for (int b = 0; b < NEB; ++b) {
@@ -462,7 +469,7 @@ __global__ __launch_bounds__(64 * kRouterWaves) void k_router_route(
       }
     }
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
+    for (int q = 0; q < NQ; ++q)
 #pragma unroll
       for (int b = 0; b < NEB; ++b) mfma16(acc[b], xa[q], wa[b][q]);
   }
@@ -474,7 +481,9 @@ __global__ __launch_bounds__(64 * kRouterWaves) void k_router_route(
   if (wave < NEB) {
     const int e = wave * 16 + rl;
     f32x4 v = red[0][wave][lane];
-#pragma unroll
+    // four LDS reads in flight (all fifteen hoisted ahead of the adds took 60
+    // VGPRs); the adds stay in wave order
+#pragma unroll 4
     for (int q = 1; q < kRouterWaves; ++q) v += red[q][wave][lane];
     const float bv = e < E && bias ? bias[e] : 0.0f;
 #pragma unroll
@@ -486,11 +495,10 @@ __global__ __launch_bounds__(64 * kRouterWaves) void k_router_route(
     const int t = t0 + wave;
     for (int e = lane; e < E; e += 64) logits[(int64_t)t * E + e] = lg[wave][e];
     float pr[1];
-    int sel[16];
+    int sel;
     route_row<1>(&lg[wave][0], t, E, k, tau, norm, probs, lse, idx, w, pr, sel);
     pl[wave][lane] = pr[0];
-    if (lane == 0)
-      for (int j = 0; j < k; ++j) atomicAdd(&hist[sel[j]], 1);
+    if (lane < k) atomicAdd(&hist[sel], 1);
   }
   __syncthreads();
   // the group's histogram and probability column sums (tokens in order)
@@ -655,97 +663,130 @@ MOE_DEV int wave_incl_scan(int v) {
 
 // With cnt[e] (LDS, e < E <= 1024) in place, a block of 1024 threads writes
 // the exclusive offsets (also to offs, LDS) and the tile prefixes of every
-// height in kTileBM, one expert per thread.  Integer arithmetic only.
+// height in kTileBM, one expert per thread.  The kScanCount scans run
+// together: a wave scan each, the wave totals to wsum[j][wave] (LDS,
+// kScanCount x 16), one barrier, and each thread adds the totals of the
+// waves below it with a fixed-trip predicated loop (its LDS reads all in
+// flight).  Integer arithmetic only.
+constexpr int kScanCount = 1 + kTilePrefixes * kNumTileBM;
 MOE_DEV void scan_counts(const int* cnt, int E, int* __restrict__ offsets,
                          int* __restrict__ tile_prefix, int* offs, int* wsum) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int j = 0; j <= kTilePrefixes * kNumTileBM; ++j) {
-    const int c = tid < E ? cnt[tid] : 0;
-    int v = c;
+  const int c = tid < E ? cnt[tid] : 0;
+  int v[kScanCount], incl[kScanCount];
+#pragma unroll
+  for (int j = 0; j < kScanCount; ++j) {
+    v[j] = c;
     if (j > 0) {
       const int bm = kTileBM[(j - 1) / kTilePrefixes], r = c % bm, kind = (j - 1) % kTilePrefixes;
-      v = kind == 0 ? (c + bm - 1) / bm
-        : kind == 1 ? c / bm + (r > bm / 2 ? 1 : 0)
-                    : (r > 0 && r <= bm / 2 ? 1 : 0);
+      v[j] = kind == 0 ? (c + bm - 1) / bm
+           : kind == 1 ? c / bm + (r > bm / 2 ? 1 : 0)
+                       : (r > 0 && r <= bm / 2 ? 1 : 0);
     }
-    const int incl = wave_incl_scan(v);
-    if (lane == 63) wsum[wave] = incl;
-    __syncthreads();
+    incl[j] = wave_incl_scan(v[j]);
+    if (lane == 63) wsum[j * 16 + wave] = incl[j];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kScanCount; ++j) {
     int base = 0;
-    for (int w = 0; w < wave; ++w) base += wsum[w];
+#pragma unroll
+    for (int w = 0; w < 15; ++w) base += w < wave ? wsum[j * 16 + w] : 0;
     int* dst = j == 0 ? offsets : tile_prefix + (j - 1) * (E + 1);
     if (tid < E) {
-      dst[tid] = base + incl - v;
-      if (j == 0) offs[tid] = base + incl - v;
+      dst[tid] = base + incl[j] - v[j];
+      if (j == 0) offs[tid] = base + incl[j] - v[j];
     }
-    if (tid == 1023) dst[E] = base + incl;
-    __syncthreads();
+    if (tid == 1023) dst[E] = base + incl[j];
   }
+  __syncthreads();
 }
 
 // One block of 1024 threads (E <= 1024).  Thread (g, e) = (tid / E, tid % E)
 // owns expert e's histogram entries of a contiguous chunk of blocks: the
-// chunk sums and their exclusive prefix over g give the expert counts and the
-// chunk bases; the expert counts are then scanned in parallel (one expert per
-// thread) for the offsets and for the tile prefix of every height in kTileBM;
-// a last pass writes every block's base.  Integer arithmetic only.
+// chunk sums and their exclusive prefix over g (a log-step scan in LDS) give
+// the expert counts and the chunk bases; the expert counts are then scanned
+// in parallel (one expert per thread) for the offsets and for the tile prefix
+// of every height in kTileBM; a last pass writes every block's base.  Chunks
+// of up to kScanRegChunk blocks stay in registers between the two passes (one
+// round of loads, all in flight); longer ones are read twice, eight loads in
+// flight.  Integer arithmetic only.
+constexpr int kScanRegChunk = 64;
 __global__ __launch_bounds__(1024) void k_scan(const int* __restrict__ block_hist, int nb, int E,
                                                int* __restrict__ block_base,
                                                int* __restrict__ counts,
                                                int* __restrict__ offsets,
                                                int* __restrict__ tile_prefix) {
   __shared__ int cnt[1024], offs[1024], part[1024];
-  __shared__ int wsum[16];
+  __shared__ int wsum[16 * kScanCount];
   const int tid = threadIdx.x;
   const int G = 1024 / E;            // threads per expert
   const int e = tid % E, g = tid / E;
   const bool act = g < G;
   const int chunk = (nb + G - 1) / G;
   const int b0 = act ? g * chunk : 0, b1 = act ? min(nb, b0 + chunk) : 0;
-  // eight independent loads in flight per step (many blocks: the fused
-  // router's 16-token groups)
-  constexpr int U = 8;
+  const int n = b1 - b0;
+  const bool in_regs = chunk <= kScanRegChunk;  // the same in every thread
+  int c[kScanRegChunk];
   int sum = 0;
-  int b = b0;
-  for (; b + U <= b1; b += U) {
-    int c[U];
+  constexpr int U = 8;
+  if (in_regs) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) c[u] = block_hist[(int64_t)(b + u) * E + e];
+    for (int u = 0; u < kScanRegChunk; ++u) c[u] = u < n ? block_hist[(int64_t)(b0 + u) * E + e] : 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u) sum += c[u];
-  }
-  for (; b < b1; ++b) sum += block_hist[(int64_t)b * E + e];
-  part[tid] = sum;
-  __syncthreads();
-  if (tid < E) {
-    int run = 0;
-    for (int q = 0; q < G; ++q) {
-      const int v = part[q * E + tid];
-      part[q * E + tid] = run;
-      run += v;
+    for (int u = 0; u < kScanRegChunk; ++u) sum += c[u];
+  } else {
+    int b = b0;
+    for (; b + U <= b1; b += U) {
+      int cu[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) cu[u] = block_hist[(int64_t)(b + u) * E + e];
+#pragma unroll
+      for (int u = 0; u < U; ++u) sum += cu[u];
     }
-    cnt[tid] = run;
-    counts[tid] = run;
+    for (; b < b1; ++b) sum += block_hist[(int64_t)b * E + e];
+  }
+  // inclusive scan of the chunk sums over g, per expert
+  part[tid] = act ? sum : 0;
+  __syncthreads();
+  for (int d = 1; d < G; d <<= 1) {
+    const int v = act && g >= d ? part[tid - d * E] : 0;
+    __syncthreads();
+    if (act) part[tid] += v;
+    __syncthreads();
+  }
+  if (tid < E) {
+    const int total = part[(G - 1) * E + tid];
+    cnt[tid] = total;
+    counts[tid] = total;
   }
   __syncthreads();
   scan_counts(cnt, E, offsets, tile_prefix, offs, wsum);
-  if (act) {
-    int run = offs[e] + part[tid];
+  if (!act) return;
+  int run = offs[e] + part[tid] - sum;
+  if (in_regs) {
+#pragma unroll
+    for (int u = 0; u < kScanRegChunk; ++u)
+      if (u < n) {
+        block_base[(int64_t)(b0 + u) * E + e] = run;
+        run += c[u];
+      }
+  } else {
     int b = b0;
     for (; b + U <= b1; b += U) {
-      int c[U];
+      int cu[U];
 #pragma unroll
-      for (int u = 0; u < U; ++u) c[u] = block_hist[(int64_t)(b + u) * E + e];
+      for (int u = 0; u < U; ++u) cu[u] = block_hist[(int64_t)(b + u) * E + e];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         block_base[(int64_t)(b + u) * E + e] = run;
-        run += c[u];
+        run += cu[u];
       }
     }
     for (; b < b1; ++b) {
-      const int c = block_hist[(int64_t)b * E + e];
+      const int cv = block_hist[(int64_t)b * E + e];
       block_base[(int64_t)b * E + e] = run;
-      run += c;
+      run += cv;
     }
   }
 }
@@ -819,7 +860,7 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(const int* __restrict__
                                                          int* __restrict__ inv_perm) {
   __shared__ int sidx[kRouteSmallTokens * 16];
   __shared__ unsigned tmask[1024][2];
-  __shared__ int cnt[1024], offs[1024], wsum[16];
+  __shared__ int cnt[1024], offs[1024], wsum[16 * kScanCount];
   const int tid = threadIdx.x;
   for (int e = tid; e < E; e += 1024) tmask[e][0] = tmask[e][1] = 0u;
   for (int i = tid; i < Tn * k; i += 1024) sidx[i] = idx[i];
