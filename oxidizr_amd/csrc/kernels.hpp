@@ -1444,7 +1444,22 @@ __global__ __launch_bounds__(256) void k_router_bwd(
 }
 
 // dx = dlogits Wr (NN, K = E) + sum_j dXp[inv_perm[t, j]] + dxs[t].
+// The whole fp32 accumulator tile is staged in LDS (rows of BN + 4 floats)
+// and read back by units of 8 outputs: 16 consecutive lanes cover 128
+// consecutive columns of one row, so every gathered dXp row segment is read
+// as whole 128-byte lines by one instruction.  (Visiting one 32-column block
+// at a time read half lines, whose other half came back from memory a block
+// later.)  KMAX >= k, a power of two, sizes the units each thread keeps in
+// flight.  Per output: the
+// accumulator, then the k gathered rows in slot order, then dxs.
 template <typename T>
+constexpr int dgrad_smem_elems() {
+  using C = typename Tilings<T>::Router;
+  constexpr int a = kernel_smem_elems<C, T, 1, 1, 1>();
+  constexpr int b = C::BM * (C::BN + 4) * 4 / (int)sizeof(T);
+  return a > b ? a : b;
+}
+template <typename T, int KMAX>
 __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, int Epad, int E,
                                                       const T* __restrict__ wr, int Tn, int H,
                                                       const T* __restrict__ dXp,
@@ -1452,58 +1467,101 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
                                                       const T* __restrict__ dxs,
                                                       T* __restrict__ dx) {
   using C = typename Tilings<T>::Router;
-  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
-  RowGroups g{nullptr, nullptr, nullptr, nullptr, 1, Tn, 0};
-  int grp, row0, mv, n0;
-  if (!resolve_rows(g, H, C::BM, C::BN, grp, row0, mv, n0)) return;
+  static_assert(C::THREADS == 256 && C::BN == 128, "16 units of 8 columns per row, 16 rows per pass");
+  __shared__ __align__(16) T smem[dgrad_smem_elems<T>()];
+  // row-major tile order: the column tiles of one row block run together, so
+  // the pieces of every gathered dXp row are read at about the same time
+  const int ntn = (H + C::BN - 1) / C::BN;
+  const int row0 = (int)(blockIdx.x / ntn) * C::BM, n0 = (int)(blockIdx.x % ntn) * C::BN;
+  if (row0 >= Tn) return;
+  const int mv = min(C::BM, Tn - row0);
   OpDesc<T> a[1] = {{dl + (int64_t)row0 * Epad, Epad, mv, Epad}};
   OpDesc<T> b[1] = {{wr + n0, H, H - n0, E}};
   f32x16 acc[1][C::TN][C::TM];
   zero_acc<C, 1>(acc);
   mainloop<C, T, false, true, 1, 1>(acc, a, b, Epad, smem);
+  // the main loop ends with a barrier: its stages are free
+  constexpr int P = C::BN + 4;
+  float* tile = reinterpret_cast<float*>(smem);
+  {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / C::WGN, wn = wave % C::WGN;
+#pragma unroll
+    for (int tn = 0; tn < C::TN; ++tn)
+#pragma unroll
+      for (int tm = 0; tm < C::TM; ++tm)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int row = wm * C::WM + tm * 32 + (lane & 31);
+          const int col = wn * C::WN + tn * 32 + 8 * qq + 4 * (lane >> 5);
+          *reinterpret_cast<f32x4*>(tile + row * P + col) =
+              f32x4{acc[0][tn][tm][4 * qq], acc[0][tn][tm][4 * qq + 1],
+                    acc[0][tn][tm][4 * qq + 2], acc[0][tn][tm][4 * qq + 3]};
+        }
+  }
+  __syncthreads();
   const int64_t TK = (int64_t)Tn * k;
-  static_assert(epi_lds_floats<C, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-  for_each_row8<C, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
-    if (m >= mv || n0 + n >= H) return;
-    const int t = row0 + m;
-    float r[8], q[8];
+  constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
+  const int cu = threadIdx.x & 15;        // unit (8 columns) of the row
+  const int n = n0 + cu * 8;
+  const bool nin = n < H;
+  // U units per step, rows r0, r0 + 16, ..., sized so that U * KMAX * NV
+  // gathered 16-byte vectors (32 for bf16, 16 for fp32) are in flight per
+  // thread
+  constexpr int UW = NV == 1 ? 32 / KMAX : 8 / KMAX;
+  constexpr int U = UW < 1 ? 1 : UW > C::BM / 16 ? C::BM / 16 : UW;
+  static_assert(U >= 1 && (C::BM / 16) % U == 0, "units per step");
+  for (int r0 = threadIdx.x >> 4; r0 < C::BM; r0 += 16 * U) {
+    u32x4 raw[U][KMAX][NV], rs[U][NV];
+    bool ok[U];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) r[i] = v[0][i];
-    // every gathered row is requested before the first one is added (k <= 16,
-    // summed in slot order)
-    constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
-    u32x4 raw[16][NV];
+    for (int h2 = 0; h2 < U; ++h2) {
+      const int r = r0 + 16 * h2;
+      ok[h2] = nin && r < mv;
+      const int t = row0 + r;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (j < k) {
-        int64_t p = inv_perm[(int64_t)t * k + j];
-        p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+      for (int j = 0; j < KMAX; ++j) {
+        if (j < k && ok[h2]) {
+          int64_t p = inv_perm[(int64_t)t * k + j];
+          p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
 #pragma unroll
-        for (int h = 0; h < NV; ++h) raw[j][h] = *gptr(reinterpret_cast<const u32x4*>(dXp + p * H + n0 + n + h * (8 / NV)));
+          for (int h = 0; h < NV; ++h)
+            raw[h2][j][h] = *gptr(reinterpret_cast<const u32x4*>(dXp + p * H + n + h * (8 / NV)));
+        }
+      }
+      if (dxs && ok[h2]) {
+#pragma unroll
+        for (int h = 0; h < NV; ++h)
+          rs[h2][h] = *gptr(reinterpret_cast<const u32x4*>(dxs + (int64_t)t * H + n + h * (8 / NV)));
       }
     }
-    u32x4 rs[NV];
-    if (dxs) {
 #pragma unroll
-      for (int h = 0; h < NV; ++h) rs[h] = *gptr(reinterpret_cast<const u32x4*>(dxs + (int64_t)t * H + n0 + n + h * (8 / NV)));
-    }
+    for (int h2 = 0; h2 < U; ++h2) {
+      if (!ok[h2]) continue;
+      const int r = r0 + 16 * h2;
+      float v[8], q[8];
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(tile + r * P + cu * 8);
+      const f32x4 hi = *reinterpret_cast<const f32x4*>(tile + r * P + cu * 8 + 4);
+      v[0] = lo[0]; v[1] = lo[1]; v[2] = lo[2]; v[3] = lo[3];
+      v[4] = hi[0]; v[5] = hi[1]; v[6] = hi[2]; v[7] = hi[3];
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      if (j < k) {
+      for (int j = 0; j < KMAX; ++j) {
+        if (j < k) {
 #pragma unroll
-        for (int h = 0; h < NV; ++h) unpack16(raw[j][h], q + h * (8 / NV), T());
+          for (int h = 0; h < NV; ++h) unpack16(raw[h2][j][h], q + h * (8 / NV), T());
 #pragma unroll
-        for (int i = 0; i < 8; ++i) r[i] += q[i];
+          for (int i = 0; i < 8; ++i) v[i] += q[i];
+        }
       }
-    }
-    if (dxs) {
+      if (dxs) {
 #pragma unroll
-      for (int h = 0; h < NV; ++h) unpack16(rs[h], q + h * (8 / NV), T());
+        for (int h = 0; h < NV; ++h) unpack16(rs[h2][h], q + h * (8 / NV), T());
 #pragma unroll
-      for (int i = 0; i < 8; ++i) r[i] += q[i];
+        for (int i = 0; i < 8; ++i) v[i] += q[i];
+      }
+      store8(dx + (int64_t)(row0 + r) * H + n, v);
     }
-    store8(dx + (int64_t)t * H + n0 + n, r);
-  });
+  }
 }
 
 __global__ void k_has_grad(const int* __restrict__ counts, int E, uint8_t* __restrict__ has_grad) {

@@ -997,9 +997,16 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   if (wait_sdx) HIP_TRY(hipStreamWaitEvent(s, p->sdx, 0));
   {
     StageTimer tm(p, s, MOE_STAGE_DX);
-    hipLaunchKernelGGL(k_router_dgrad<D>, dim3(ceil_div(T, CR::BM) * ceil_div(H, CR::BN)),
-                       dim3(256), 0, s, dlt, Epad, E, (const D*)w->router, T, H, dXp, inv, k, dxs,
-                       dx);
+    const dim3 grid(ceil_div(T, CR::BM) * ceil_div(H, CR::BN));
+    const D* wr = (const D*)w->router;
+    if (k <= 2)
+      hipLaunchKernelGGL((k_router_dgrad<D, 2>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+    else if (k <= 4)
+      hipLaunchKernelGGL((k_router_dgrad<D, 4>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+    else if (k <= 8)
+      hipLaunchKernelGGL((k_router_dgrad<D, 8>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+    else
+      hipLaunchKernelGGL((k_router_dgrad<D, 16>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
     if (has_grad) hipLaunchKernelGGL(k_has_grad, dim3(ceil_div(E, 256)), dim3(256), 0, s, counts, E, has_grad);
     LAUNCH_CHECK();
   }
