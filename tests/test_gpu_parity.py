@@ -104,6 +104,7 @@ FP32_CASES = [
          shared_scale=0.5, aux_switch=0.3, aux_sqprob=2.0),
     dict(T=1024, H=384, E=8, k=2, I=1024, S=0),     # BASELINE config 1 (fp32, CPU-runnable)
     dict(T=33, H=136, E=12, k=12, I=16, S=0),       # k == E: every expert selected
+    dict(T=150, H=64, E=10, k=6, I=32, S=16),       # 4 < k <= 8 (dx gathers sized for k <= 8)
 ]
 
 
@@ -139,7 +140,7 @@ BF16_CASES = [
     # after every full tile (the tail order of configs 2 and 3)
     dict(T=1300, H=128, E=4, k=3, I=96, S=32, bias=True, half_last=True),
     dict(T=1280, H=136, E=4, k=2, I=200, S=0, half_last=True),
-    # k above what dx prefetches per row group (bf16: 8)
+    # k above 8: dx's gathers sized for k <= 16
     dict(T=160, H=64, E=12, k=10, I=48, S=16),
     # fused router with a partial last expert block (E = 40) and router bias
     dict(T=300, H=200, E=40, k=4, I=64, S=0, bias=True),
