@@ -941,11 +941,14 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // (ThreeQuarterRows, a 2 x 2 wave grid of 3BM/8-row blocks), so the MFMAs
 // spend no more than BM/4 rows on padding.  Config 5's ~256-row experts run
 // 79 % useful rows with BM/2 granularity and 94 % with BM/4.  Every output
-// element keeps its k order (same bits).  bf16 256-row tiles only.
+// element keeps its k order (same bits).  bf16 256-row tiles only.  The BM/4-
+// and BM/2-row tilings (40 and 48 KB per k-tile) run three LDS stages, within
+// the LDS the full tile's epilogue already takes (config 5 gate/up forward
+// 5.06 -> 4.87 ms; four stages for BM/4 were no faster).
 template <class C>
-using QuarterRows = Tiling<bf16_t, C::BM / 4, C::BN, C::BK, 4, C::NST, C::NW>;
+using QuarterRows = Tiling<bf16_t, C::BM / 4, C::BN, C::BK, 4, 3, C::NW>;
 template <class C>
-using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4, C::NST, C::NW>;
+using HalfRows = Tiling<bf16_t, C::BM / 2, C::BN, C::BK, 4, 3, C::NW>;
 template <class C>
 using ThreeQuarterRows = Tiling<bf16_t, 3 * C::BM / 4, C::BN, C::BK, C::NW / 2, C::NST, C::NW>;
 template <typename T, class C>
@@ -995,10 +998,11 @@ MOE_DEV void with_tile_rows(int mv, F&& body) {
 }
 // Likewise along N: a 256-column tile with at most 128 valid columns (the
 // last tile column when N % 256 is in 1..128, e.g. I = 1408) runs as a
-// 128-column tile with the four waves stacked along M (HalfCols<C>), with the
-// same per-element k order (same bits).  bf16 256-column tiles only.
+// 128-column tile with the waves stacked along M (HalfCols<C>, three LDS
+// stages), with the same per-element k order (same bits).  bf16 256-column
+// tiles only.
 template <class C>
-using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, C::NW / 4, C::NST, C::NW>;
+using HalfCols = Tiling<bf16_t, C::BM, C::BN / 2, C::BK, C::NW / 4, 3, C::NW>;
 template <typename T, class C>
 constexpr bool has_half_cols() { return sizeof(T) == 2 && C::BN == 256; }
 template <typename T, class C, int NA, int NB, int NACC>
