@@ -34,8 +34,12 @@ namespace moe {
 // weight gradient 14 % slower.  Router-sized GEMMs (one side = E) keep
 // 128 x 128 and four waves.  fp32 keeps four waves.
 template <typename T> struct Tilings;
+// RouterNarrow: 64-row router tiles with four stages, for launches whose
+// 128-row grid would leave CUs idle (config 5: 128 -> 256 workgroups, router
+// GEMM 120.7 -> 105 us; two stages 107.5 us).
 template <> struct Tilings<bf16_t> {
   using Router = Tiling<bf16_t, 128, 128, 64>;
+  using RouterNarrow = Tiling<bf16_t, 64, 128, 64, 4, 4>;
   using GateUp = Tiling<bf16_t, 256, 128, 64, 2, 2, 8>;
   using Big = Tiling<bf16_t, 256, 256, 64, 2, 2, 8>;
   using WgradPair = Tiling<bf16_t, 128, 256, 64, 2, 2, 8>;
@@ -46,6 +50,7 @@ template <> struct Tilings<bf16_t> {
 // weight-gradient pair they measured no faster.
 template <> struct Tilings<float> {
   using Router = Tiling<float, 128, 128, 32>;
+  using RouterNarrow = Router;
   using GateUp = Tiling<float, 128, 64, 32>;
   using Big = Tiling<float, 128, 64, 32>;
   using WgradPair = Tiling<float, 128, 128, 32>;
@@ -285,14 +290,14 @@ MOE_DEV T* pick(T* const* tab, T* single, int g) {
 }
 
 // ------------------------------------------------------------------ router GEMM
-// logits[t, e] = x[t] . Wr[e] (+ bias[e]), fp32 out.
-template <typename T>
+// logits[t, e] = x[t] . Wr[e] (+ bias[e]), fp32 out.  C: Router or
+// RouterNarrow (same per-element k order, same bits).
+template <typename T, class C = typename Tilings<T>::Router>
 __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
                                                        const T* __restrict__ wr,
                                                        const float* __restrict__ bias,
                                                        float* __restrict__ logits, int Tn, int H,
                                                        int E) {
-  using C = typename Tilings<T>::Router;
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
   RowGroups g{nullptr, nullptr, nullptr, nullptr, 1, Tn, 0};
   int grp, row0, mv, n0;

@@ -777,9 +777,16 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
                          st.logits, T, H, E);
     } else {
+      using CRN = typename Tilings<D>::RouterNarrow;
+      const float* rbias = c.has_router_bias ? w->router_bias : nullptr;
       const int grid = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
-      hipLaunchKernelGGL(k_router_logits<D>, dim3(grid), dim3(256), 0, s, x, (const D*)w->router,
-                         c.has_router_bias ? w->router_bias : nullptr, st.logits, T, H, E);
+      if (grid < 256) {  // fewer 128-row tiles than CUs
+        hipLaunchKernelGGL((k_router_logits<D, CRN>), dim3(ceil_div(T, CRN::BM) * ceil_div(E, CRN::BN)),
+                           dim3(CRN::THREADS), 0, s, x, (const D*)w->router, rbias, st.logits, T, H, E);
+      } else {
+        hipLaunchKernelGGL((k_router_logits<D, CR>), dim3(grid), dim3(CR::THREADS), 0, s, x,
+                           (const D*)w->router, rbias, st.logits, T, H, E);
+      }
     }
     LAUNCH_CHECK();
   }
