@@ -127,11 +127,13 @@ SplitPlan plan_split(int M, int N, int K) {
 
 // fp32 partial-tile bytes of the largest dense weight gradient of one backward:
 // the router's, or the shared expert's (they run concurrently, on separate
-// buffers).
+// buffers).  Planned with the tilings the launches use (WgradTiling), so the
+// split counts agree; launch_dense_wgrad also refuses a split that would not
+// fit.
 template <typename D>
 size_t splitk_bytes(const moe_config& c, int64_t T, bool shared) {
-  using CB = typename Tilings<D>::Big;
-  using CW = typename Tilings<D>::WgradPair;
+  using CB = WgradTiling<D, 1>;
+  using CW = WgradTiling<D, 2>;
   const int H = c.hidden, E = c.num_experts, S = c.shared_intermediate;
   size_t most = 0;
   auto need = [&](SplitPlan sp, int na, int M, int N) {
@@ -533,13 +535,23 @@ inline int kgrouped_grid(int groups, int M, int N, int BM, int BN) {
 }
 
 // Weight gradient of a dense (all-token) GEMM: out_x[m, n] = alpha * sum_t
-// P_x[t, m] Q[t, n], split over tokens when that fills the GPU better.
+// P_x[t, m] Q[t, n], split over tokens when that fills the GPU better.  The
+// fp32 partials of a split must fit the partial_bytes of `partial` (else an
+// error, before anything is launched).
 template <typename D, int NA>
-void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, const D* Q,
-                        int64_t ldq, int T, int M, int N, float alpha, D* o0, D* o1,
-                        float* partial) {
+moe_status launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, const D* Q,
+                              int64_t ldq, int T, int M, int N, float alpha, D* o0, D* o1,
+                              float* partial, size_t partial_bytes) {
   using C = WgradTiling<D, NA>;
   const SplitPlan sp = plan_split<C>(M, N, T);
+  if (sp.nsplit > 1) {
+    const size_t need = (size_t)NA * sp.nsplit * (size_t)M * N * 4;
+    if (need > partial_bytes)
+      return fail(MOE_ERR_UNSUPPORTED,
+                  "weight-gradient split of %d chunks needs %zu bytes of partials, the workspace "
+                  "holds %zu",
+                  sp.nsplit, need, partial_bytes);
+  }
   const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk, 1, nullptr};
   hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN)),
                      dim3(C::THREADS), 0, s, P0, P1, ldp, Q,
@@ -549,6 +561,8 @@ void launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t ldp, co
     hipLaunchKernelGGL(k_splitk_reduce<D>, dim3(ceil_div(MN, 2048), NA), dim3(256), 0, s, partial,
                        sp.nsplit, MN, alpha, o0, o1);
   }
+  LAUNCH_CHECK();
+  return MOE_OK;
 }
 
 // Pointers to the routing state and the activations of one call.  The
@@ -910,11 +924,13 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
       HIP_TRY(hipEventRecord(p->sdx, ss));
       wait_sdx = true;
     }
-    launch_dense_wgrad<D, 1>(ss, dout, nullptr, H, sA, S, T, H, S, sc, (D*)g->shared_down, nullptr,
-                             partial_sh);
-    launch_dense_wgrad<D, 2>(ss, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
-                             (D*)g->shared_up, partial_sh);
-    LAUNCH_CHECK();
+    const size_t cap_sh = splitk_bytes<D>(c, T, true);
+    moe_status rs = launch_dense_wgrad<D, 1>(ss, dout, nullptr, H, sA, S, T, H, S, sc,
+                                             (D*)g->shared_down, nullptr, partial_sh, cap_sh);
+    if (rs != MOE_OK) return rs;
+    rs = launch_dense_wgrad<D, 2>(ss, sdG, sdU, S, x, H, T, S, H, 1.0f, (D*)g->shared_gate,
+                                  (D*)g->shared_up, partial_sh, cap_sh);
+    if (rs != MOE_OK) return rs;
   }
   if (recompute) {
     moe_status r = routed_fwd<D>(p, s, T, x, st, false);
@@ -987,8 +1003,10 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
       default: launch_router_bwd<16, D>(s, grid, probs, lse, idx, topw, dw, P, counts, d_aux, d_z, T, E, Epad, k, c, dl, dlt); break;
     }
     LAUNCH_CHECK();
-    launch_dense_wgrad<D, 1>(s, dlt, nullptr, Epad, x, H, T, E, H, 1.0f, (D*)g->router, nullptr,
-                             partial);
+    const moe_status rr = launch_dense_wgrad<D, 1>(s, dlt, nullptr, Epad, x, H, T, E, H, 1.0f,
+                                                   (D*)g->router, nullptr, partial,
+                                                   splitk_bytes<D>(c, T, false));
+    if (rr != MOE_OK) return rr;
     if (c.has_router_bias && g->router_bias) {
       const int nrb = ceil_div(T, 64);
       float* part = (float*)(ws);  // column partials at workspace offset 0
