@@ -7,7 +7,7 @@
  * (out, aux_loss, z_loss) and whose backward is the boostr autograd graph
  * walked by `backward_wrt` (src/trainer.rs:1097).  A Rust wrapper keeps that
  * struct, its constructors and config keys, and calls these entry points
- * through a thin FFI crate; see INTEGRATION.md.
+ * through a thin FFI crate (rust/moe-hip-sys).
  *
  * Conventions
  *  - Every tensor argument is a DEVICE pointer, 16-byte aligned, row-major
