@@ -174,9 +174,10 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
 // chunks in ascending order, so the result does not depend on scheduling.
 // col_walk: an XCD's tiles of a group run in tile_order (GM row tiles down a
 // column, then right) instead of row by row.  Measured on the weight
-// gradients: faster for the dense ones (shared expert: 1-3 %) and for groups
-// of >= 512 rows (configs 2 and 3: step -1.1 % / -0.4 %), slower for
-// config 5's ~256-row groups (gate/up pair +5 %).
+// gradients: faster for the dense ones (shared expert: 1-3 %), for groups of
+// >= 512 rows (configs 2 and 3: step -1.1 % / -0.4 %) and for the down
+// projection's at every size (config 5: 3.52 -> 3.42 ms); slower for the
+// gate/up pair's whole experts of ~256 rows (config 5: 5.94 -> 6.06 ms).
 // xcd_order (grouped, G a multiple of 8): when not null and its flag
 // xcd_order[G] is set, XCD x runs the whole groups xcd_order[x * G / 8 + j],
 // j < G / 8 (k_xcd_order), one after another, instead of 1/8 of every group.
