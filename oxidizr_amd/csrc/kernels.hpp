@@ -915,7 +915,9 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(const int* __restrict__
   }
 }
 
-// x_perm[pos] = x[perm[pos] / k]; one wave per row, 16-byte vectors.
+// x_perm[pos] = x[perm[pos] / k]; one wave per row, 16-byte vectors, up to
+// eight per lane loaded before any is stored (one at a time, each store
+// waited for its own load: config 5 312 -> 289 us).
 template <typename T>
 __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
                                                 const int* __restrict__ perm, int Tn, int k,
@@ -929,7 +931,17 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
   tok = tok < 0 ? 0 : (tok >= Tn ? Tn - 1 : tok);
   const T* src = x + (int64_t)tok * H;
   T* dst = xp + pos * H;
-  for (int c = lane; c < H / V; c += 64) st16(dst + c * V, ld16(src + c * V));
+  constexpr int U = 8;
+  const int nv = H / V;
+  for (int c0 = lane; c0 < nv; c0 += 64 * U) {
+    u32x4 buf[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c0 + 64 * u < nv) buf[u] = ld16(src + (c0 + 64 * u) * V);
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c0 + 64 * u < nv) st16(dst + (c0 + 64 * u) * V, buf[u]);
+  }
 }
 
 // ------------------------------------------------------------------ expert GEMMs (forward)
