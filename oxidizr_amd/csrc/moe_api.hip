@@ -847,7 +847,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                          uint8_t* has_grad) {
   using CR = typename Tilings<D>::Router;
   using CB = typename Tilings<D>::Big;
-  using CW = typename Tilings<D>::WgradPair;
+  using CS = WgradTiling<D, 1>;  // grouped weight gradients: single, pair
+  using CW = WgradTiling<D, 2>;
   const moe_config& c = p->cfg;
   const int T = (int)T64, H = c.hidden, E = c.num_experts, k = c.experts_per_tok,
             I = c.intermediate, S = c.shared_intermediate;
@@ -956,13 +957,13 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
-    const int grid = kgrouped_grid(E, H, I, CB::BM, CB::BN);
+    const int grid = kgrouped_grid(E, H, I, CS::BM, CS::BN);
     // the down projection's weight gradient walks its tiles down columns for
     // every group size (config 5's ~256-row groups: 3.52 -> 3.42 ms in a
     // probe; the gate/up pair keeps the size rule of kg)
     KGroups kgd = kg;
     kgd.col_walk = 1;
-    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(CB::THREADS), 0, ws2, dY, nullptr, (int64_t)H, A,
+    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(CS::THREADS), 0, ws2, dY, nullptr, (int64_t)H, A,
                        (int64_t)I, kgd, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
   }
