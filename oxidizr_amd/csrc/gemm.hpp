@@ -276,6 +276,8 @@ template <class C, typename T, int R>
 struct DmaStagerT {
   static_assert(sizeof(T) == 2, "transposing LDS reads are 16-bit");
   static constexpr int SPR = R / 8;              // 16-byte slots per k-row
+  // tr_swz XORs slot indices with 4 (k & 3): a k-row needs at least 16 slots
+  static_assert(SPR >= 16 && SPR <= 64, "K-major tiles of 128 to 512 columns");
   static constexpr int RPI = 64 / SPR;           // k-rows per 1 KB instruction
   static constexpr int PER = C::BK / (C::NW * RPI);  // instructions per wave per k-tile
   static_assert(PER >= 1 && C::BK % (C::NW * RPI) == 0, "k-rows must cover the waves");
