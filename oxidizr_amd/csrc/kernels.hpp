@@ -915,22 +915,21 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(const int* __restrict__
   }
 }
 
-// x_perm[pos] = x[perm[pos] / k]; one wave per row, 16-byte vectors, up to
-// eight per lane loaded before any is stored (one at a time, each store
-// waited for its own load: config 5 312 -> 289 us).
+// x_perm[inv_perm[t * k + j]] = x[t] for j < k: one wave per token reads its
+// row once (16-byte vectors, up to eight per lane in flight) and writes it to
+// the token's k slots of the permuted layout.  Reading each row once instead
+// of k times (a wave per permuted row) keeps x out of the write stream's way
+// in the caches.
 template <typename T>
 __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
-                                                const int* __restrict__ perm, int Tn, int k,
+                                                const int* __restrict__ inv_perm, int Tn, int k,
                                                 int H, T* __restrict__ xp) {
   constexpr int V = Vec16<T>::N;
-  const int64_t TK = (int64_t)Tn * k;
-  const int64_t pos = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (pos >= TK) return;
+  const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (t >= Tn) return;
   const int lane = threadIdx.x & 63;
-  int tok = perm[pos] / k;
-  tok = tok < 0 ? 0 : (tok >= Tn ? Tn - 1 : tok);
-  const T* src = x + (int64_t)tok * H;
-  T* dst = xp + pos * H;
+  const int64_t TK = (int64_t)Tn * k;
+  const T* src = x + (int64_t)t * H;
   constexpr int U = 8;
   const int nv = H / V;
   for (int c0 = lane; c0 < nv; c0 += 64 * U) {
@@ -938,9 +937,14 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 #pragma unroll
     for (int u = 0; u < U; ++u)
       if (c0 + 64 * u < nv) buf[u] = ld16(src + (c0 + 64 * u) * V);
+    for (int j = 0; j < k; ++j) {
+      const int pos = inv_perm[(int64_t)t * k + j];
+      if (pos < 0 || pos >= TK) continue;
+      T* dst = xp + (int64_t)pos * H;
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (c0 + 64 * u < nv) st16(dst + (c0 + 64 * u) * V, buf[u]);
+      for (int u = 0; u < U; ++u)
+        if (c0 + 64 * u < nv) st16(dst + (c0 + 64 * u) * V, buf[u]);
+    }
   }
 }
 

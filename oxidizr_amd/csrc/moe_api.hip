@@ -681,7 +681,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   const bool gather = !skinny || st.G != nullptr;
   if (gather) {
     StageTimer tm(p, s, stage(MOE_STAGE_GATHER));
-    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(TK, 4)), dim3(256), 0, s, x, st.perm, T, k, H,
+    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.inv, T, k, H,
                        st.xp);
     LAUNCH_CHECK();
   }
