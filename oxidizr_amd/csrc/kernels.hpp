@@ -318,6 +318,54 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
   });
 }
 
+// Split-K router GEMM for wide H with too few output tiles to fill the CUs
+// (T / 128 x E / 128 of them): partial[s][t][e] = x[t, ks) . Wr[e, ks) over
+// the s-th kchunk-column chunk of H, ks = s * kchunk (a multiple of C::BK);
+// k_router_reduce adds the chunks in order, then the bias.  The chunking
+// depends on H only, so a token's logits are the same bits in any batch.
+template <typename T, class C>
+__global__ __launch_bounds__(C::THREADS) void k_router_logits_split(const T* __restrict__ x,
+                                                                    const T* __restrict__ wr,
+                                                                    float* __restrict__ partial,
+                                                                    int Tn, int H, int E,
+                                                                    int kchunk) {
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
+  const int nN = (E + C::BN - 1) / C::BN;
+  const int tiles = ((Tn + C::BM - 1) / C::BM) * nN;
+  const int split = (int)blockIdx.x / tiles, id = (int)blockIdx.x - split * tiles;
+  const int row0 = (id / nN) * C::BM, n0 = (id % nN) * C::BN;
+  const int k0 = split * kchunk;
+  const int kv = min(kchunk, H - k0);
+  if (row0 >= Tn || kv <= 0) return;
+  const int mv = min(C::BM, Tn - row0);
+  OpDesc<T> a[1] = {{x + (int64_t)row0 * H + k0, H, mv, kv}};
+  OpDesc<T> b[1] = {{wr + (int64_t)n0 * H + k0, H, E - n0, kv}};
+  f32x16 acc[1][C::TN][C::TM];
+  zero_acc<C, 1>(acc);
+  mainloop<C, T, false, false, 1, 1>(acc, a, b, kv, smem);
+  float* out = partial + (int64_t)split * Tn * E;
+  for_each_frag<C, 1>(acc, [&](int m, int n, auto& v) {
+    if (m >= mv) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int e = n0 + n + i;
+      if (e < E) out[(int64_t)(row0 + m) * E + e] = v[0][i];
+    }
+  });
+}
+
+// logits[i] = ((partial[0][i] + partial[1][i]) + ...) + bias[i % E]
+__global__ __launch_bounds__(256) void k_router_reduce(const float* __restrict__ partial,
+                                                       int nsplit, int64_t TE, int E,
+                                                       const float* __restrict__ bias,
+                                                       float* __restrict__ logits) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= TE) return;
+  float v = partial[i];
+  for (int s = 1; s < nsplit; ++s) v += partial[(int64_t)s * TE + i];
+  logits[i] = v + (bias ? bias[i % E] : 0.0f);
+}
+
 // ------------------------------------------------------------------ routing
 // One wave routes token t: softmax(logits / tau), log-sum-exp, top-k on the
 // raw logits (NaN selects as -inf; equal values -> lower expert index first).

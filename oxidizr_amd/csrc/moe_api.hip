@@ -67,7 +67,7 @@ struct SavedLayout {
 
 struct WsLayout {
   // forward
-  size_t block_hist, block_base, colpart, ghist, gbase, gpart, sY, infer;
+  size_t block_hist, block_base, colpart, ghist, gbase, gpart, rpart, sY, infer;
   // backward
   size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
       recomp, dxm, dwn, dwn_a, dwn_b, xorder;
@@ -88,6 +88,18 @@ bool fused_router(const moe_config& c, int64_t T) {
   return c.dtype == MOE_DTYPE_BF16 && c.num_experts <= kFusedRouterMaxExperts &&
          T > kRouteSmallTokens;
 }
+// Chunks of H the tiled router GEMM splits its k-loop into (k_router_logits_split):
+// one per 1792 columns from H = 3584 up (config 5: 7168 -> 4 chunks of 28
+// k-tiles), so its T / 128 x E / 128 tiles fill the CUs.  Depends on H only.
+int router_splits(const moe_config& c) {
+  return c.hidden >= 3584 ? std::min(8, c.hidden / 1792) : 1;
+}
+template <class C>
+int router_kchunk(const moe_config& c) {
+  const int n = router_splits(c);
+  return ((c.hidden + n - 1) / n + C::BK - 1) / C::BK * C::BK;
+}
+
 // Buffer loads take 32-bit byte offsets and kOobOffset (2^31) must lie beyond
 // every resource: no operand extent may reach this many bytes.
 constexpr int64_t kMaxExtentBytes = int64_t(1) << 31;
@@ -265,6 +277,9 @@ struct moe_plan {
     L.ghist = f.take(4 * ng);
     L.gbase = f.take(4 * ng);
     L.gpart = f.take(4 * ng);
+    // split router GEMM: fp32 partial logits per chunk of H
+    const int rs = fused_router(cfg, T) ? 1 : router_splits(cfg);
+    L.rpart = f.take(rs > 1 ? 4 * (size_t)rs * T * E : 0);
     L.sY = f.take(b * T * H);
     // forward-only calls keep their routing and activations here, clear of
     // the forward scratch above (the backward regions below are unused then)
@@ -790,6 +805,15 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                          dim3(64 * kRouterWaves), 0, s, (const bf16_t*)x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
                          st.logits, T, H, E);
+    } else if (router_splits(c) > 1) {
+      const int ns = router_splits(c);
+      float* part = (float*)(ws + W.rpart);
+      const int tiles = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
+      hipLaunchKernelGGL((k_router_logits_split<D, CR>), dim3(tiles * ns), dim3(CR::THREADS), 0, s,
+                         x, (const D*)w->router, part, T, H, E, router_kchunk<CR>(c));
+      const int64_t TE = (int64_t)T * E;
+      hipLaunchKernelGGL(k_router_reduce, dim3(ceil_div(TE, 256)), dim3(256), 0, s, part, ns, TE, E,
+                         c.has_router_bias ? w->router_bias : nullptr, st.logits);
     } else {
       using CRN = typename Tilings<D>::RouterNarrow;
       const float* rbias = c.has_router_bias ? w->router_bias : nullptr;

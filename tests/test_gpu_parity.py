@@ -105,6 +105,7 @@ FP32_CASES = [
     dict(T=1024, H=384, E=8, k=2, I=1024, S=0),     # BASELINE config 1 (fp32, CPU-runnable)
     dict(T=33, H=136, E=12, k=12, I=16, S=0),       # k == E: every expert selected
     dict(T=150, H=64, E=10, k=6, I=32, S=16),       # 4 < k <= 8 (dx gathers sized for k <= 8)
+    dict(T=130, H=3592, E=6, k=2, I=32, S=0, bias=True),  # router k-loop split in two chunks
 ]
 
 
@@ -144,6 +145,9 @@ BF16_CASES = [
     dict(T=160, H=64, E=12, k=10, I=48, S=16),
     # fused router with a partial last expert block (E = 40) and router bias
     dict(T=300, H=200, E=40, k=4, I=64, S=0, bias=True),
+    # tiled router (E > 64) with its k-loop split in four chunks (H >= 7168),
+    # a partial last 128-row tile and a partial expert tile (E = 136)
+    dict(T=200, H=7176, E=136, k=4, I=32, S=16, bias=True),
 ]
 
 
