@@ -225,11 +225,13 @@ def test_shared_stream_overlap_is_bitwise_serial(dtype, S, E):
     case = Case(T=640, H=128, E=E, k=2, I=64, S=S, dtype=dtype, w_std=0.05, seed=5)
     a = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=True)
     b = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=False)
+    c = gpu_run(case, d_aux=0.01, d_z=0.001, overlap=2)  # shared-expert stream only
     names = ["out", "aux", "z", "dx", "router", "gate", "up", "down"]
     if S:
         names += ["shared_gate", "shared_up", "shared_down"]
     for n in names:
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+        np.testing.assert_array_equal(np.nan_to_num(c[n]), np.nan_to_num(b[n]), err_msg=n)
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
