@@ -106,6 +106,7 @@ FP32_CASES = [
     dict(T=33, H=136, E=12, k=12, I=16, S=0),       # k == E: every expert selected
     dict(T=150, H=64, E=10, k=6, I=32, S=16),       # 4 < k <= 8 (dx gathers sized for k <= 8)
     dict(T=130, H=3592, E=6, k=2, I=32, S=0, bias=True),  # router k-loop split in two chunks
+    dict(T=200, H=64, E=1020, k=5, I=16, S=16),     # E not a multiple of 8, most experts empty
 ]
 
 
@@ -148,6 +149,8 @@ BF16_CASES = [
     # tiled router (E > 64) with its k-loop split in four chunks (H >= 7168),
     # a partial last 128-row tile and a partial expert tile (E = 136)
     dict(T=200, H=7176, E=136, k=4, I=32, S=16, bias=True),
+    # the largest plan limits: E = 1024 experts, k = 16
+    dict(T=300, H=64, E=1024, k=16, I=16, S=0),
 ]
 
 
@@ -504,8 +507,8 @@ def test_moe_layer_autograd_backward_matches_oracle(dtype):
     o = oracle_run(case, logits, d_aux=0.01, d_z=0.001)
     tol = 1e-5 if dtype == "f32" else 1e-2
     errs = {"out": rel(out.detach().float().cpu().numpy().reshape(120, 64), o["out"]),
-            "aux": abs(float(aux) - o["aux"]) / abs(o["aux"]),
-            "z": abs(float(z) - o["z"]) / abs(o["z"]),
+            "aux": abs(float(aux.detach()) - o["aux"]) / abs(o["aux"]),
+            "z": abs(float(z.detach()) - o["z"]) / abs(o["z"]),
             "dx": rel(x.grad.float().cpu().numpy().reshape(120, 64), o["x"]),
             "router": rel(layer.router.gate.weight.grad.float().cpu().numpy(), o["router"]),
             "router_bias": rel(layer.router.bias.grad.float().cpu().numpy(), o["router_bias"])}
