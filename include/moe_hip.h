@@ -231,9 +231,8 @@ typedef enum {
 } moe_stage;
 const char* moe_stage_name(int32_t stage);
 moe_status moe_plan_set_profiling(moe_plan* plan, int32_t stage_mask);
-/* The shared expert (and, after its backward, the routed down projection's
- * weight gradient) runs on a second stream of the plan, and the backward's
- * gate/up weight gradients on a third (each forked from and joined back into
+/* The shared expert runs on a second stream of the plan, and the backward's
+ * routed weight gradients on a third (each forked from and joined back into
  * the call's stream inside every call), so that independent GEMMs fill each
  * other's partial rounds of work.  on = 0 runs everything on the call's
  * stream instead (serial order, for per-kernel measurements); on = 2 uses the

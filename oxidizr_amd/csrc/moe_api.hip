@@ -198,11 +198,9 @@ struct moe_plan {
   hipStream_t aux = nullptr;
   hipEvent_t fork = nullptr, join = nullptr;
   hipEvent_t sdx = nullptr;  // backward: the shared expert's input gradient is ready
-  // The backward's gate/up weight gradient needs only dG / dU and the
-  // routing state: it runs on a third stream, beside the input-gradient GEMMs
-  // of the call's stream (the down projection's weight gradient follows the
-  // shared expert's backward on the second stream, or runs on the third when
-  // there is no shared expert).
+  // The backward's routed weight gradients need only dY / dG / dU and the
+  // routing state: they run on a third stream, beside the input-gradient
+  // GEMMs and the router backward on the call's stream.
   // In the forward the same stream sums the mean router probabilities (needed
   // only by the losses) while the call's stream dispatches.
   hipStream_t wgs = nullptr;
@@ -969,11 +967,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                        topw, T, k, H, dw, dY);
     LAUNCH_CHECK();
   }
-  // From here the routed weight gradients run beside s (they read dY, A,
-  // X_perm and, after the down projection's input gradient, dG / dU): the
-  // gate/up pair on the weight-gradient stream ws2, the down projection's on
-  // the shared expert's stream (ws2 without a shared expert); the input
-  // gradients and the router backward stay on s.
+  // From here the routed weight gradients run on the weight-gradient stream
+  // ws2 (they read dY, A, X_perm and, after the down projection's input
+  // gradient, dG / dU); the input gradients and the router backward on s.
   const hipStream_t ws2 = p->wgrad_stream(s);
   HIP_TRY(wgrad_join.fork(s, ws2, p->wfork, p->wjoin));
   // whole experts per XCD for the gate/up weight gradient when the experts
@@ -984,23 +980,14 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     LAUNCH_CHECK();
   }
   {
-    // the down projection's weight gradient follows the shared expert's
-    // backward on its stream (when there is one), so that the gate/up pair on
-    // ws2 can start as soon as dG / dU exist and runs beside the gate/up input
-    // gradient (config 5 step -0.1 to -0.3 %, config 2 -0.3 to -0.6 %)
-    const hipStream_t dws = S > 0 ? p->shared_stream(s) : ws2;
-    if (dws != s && dws != ws2) {  // dY is ready on s
-      HIP_TRY(hipEventRecord(p->wfork, s));
-      HIP_TRY(hipStreamWaitEvent(dws, p->wfork, 0));
-    }
-    StageTimer tm(p, dws, MOE_STAGE_DOWN_WGRAD);
+    StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
     const int grid = kgrouped_grid(E, H, I, CS::BM, CS::BN);
     // the down projection's weight gradient walks its tiles down columns for
     // every group size (config 5's ~256-row groups: 3.52 -> 3.42 ms in a
     // probe; the gate/up pair keeps the size rule of kg)
     KGroups kgd = kg;
     kgd.col_walk = 1;
-    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(CS::THREADS), 0, dws, dY, nullptr, (int64_t)H, A,
+    hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(CS::THREADS), 0, ws2, dY, nullptr, (int64_t)H, A,
                        (int64_t)I, kgd, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
     LAUNCH_CHECK();
   }
