@@ -191,8 +191,8 @@ struct KGroups {
   const int* xcd_order;
 };
 
-MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp, int& split,
-                       int& krow0, int& K, int& m0, int& n0) {
+MOE_DEV bool resolve_k(const KGroups& g, int blk, int M, int N, int BM, int BN, int& grp,
+                       int& split, int& krow0, int& K, int& m0, int& n0) {
   const int nM = (M + BM - 1) / BM, nN = (N + BN - 1) / BN;
   // Each group (or split chunk) owns 8 * ceil(per / 8) consecutive blocks and
   // its per tiles are dealt over the 8 XCDs in contiguous ranges, so every XCD
@@ -205,15 +205,15 @@ MOE_DEV bool resolve_k(const KGroups& g, int M, int N, int BM, int BN, int& grp,
     // whole groups per XCD: block b runs on XCD b % 8 and is that XCD's
     // (b / 8)-th block; the grid of 8 * ceil(per / 8) blocks per group covers
     // G / 8 groups of per tiles on every XCD
-    const int epx = g.G >> 3, local = (int)(blockIdx.x >> 3);
+    const int epx = g.G >> 3, local = (blk >> 3);
     const int j = uni(local / per);
     if (j >= epx) return false;
     r = uni(local - j * per);
-    gs = uni(g.xcd_order[(int)(blockIdx.x & 7) * epx + j]);
+    gs = uni(g.xcd_order[(blk & 7) * epx + j]);
   } else {
     const int span = 8 * ((per + 7) >> 3);
-    gs = uni(blockIdx.x / span);
-    if (!xcd_slot(blockIdx.x - gs * span, per, r)) return false;
+    gs = uni(blk / span);
+    if (!xcd_slot(blk - gs * span, per, r)) return false;
   }
   if (g.col_walk) {
     int mt, nt;
@@ -1377,16 +1377,13 @@ template <typename T, int NA>
 using WgradTiling = typename std::conditional<NA == 2, typename Tilings<T>::WgradPair,
                                               typename Tilings<T>::Big>::type;
 template <typename T, int NA, bool GROUPED>
-__global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
-                                               int64_t ldp, const T* __restrict__ Q, int64_t ldq,
-                                               KGroups groups, int M, int N, float alpha,
-                                               T* const* out0_tab, T* out0_one,
-                                               T* const* out1_tab, T* out1_one,
-                                               float* __restrict__ partial) {
+MOE_DEV void wgrad_tile(T* smem, int blk, const T* __restrict__ P0, const T* __restrict__ P1,
+                        int64_t ldp, const T* __restrict__ Q, int64_t ldq, const KGroups& groups,
+                        int M, int N, float alpha, T* const* out0_tab, T* out0_one,
+                        T* const* out1_tab, T* out1_one, float* __restrict__ partial) {
   using C = WgradTiling<T, NA>;
-  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, NA, 1, NA>()];
   int grp, split, krow0, K, m0, n0;
-  if (!resolve_k(groups, M, N, C::BM, C::BN, grp, split, krow0, K, m0, n0)) return;
+  if (!resolve_k(groups, blk, M, N, C::BM, C::BN, grp, split, krow0, K, m0, n0)) return;
   OpDesc<T> a[NA];
   a[0] = {P0 + krow0 * ldp + m0, ldp, M - m0, K};
   if constexpr (NA == 2) a[1] = {P1 + krow0 * ldp + m0, ldp, M - m0, K};
@@ -1402,7 +1399,7 @@ __global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T
     // value; the bf16 staging halves the epilogue's LDS traffic.  The packing
     // copies the accumulators into VGPRs, which spilled while the split
     // branch below shared the kernel; here that branch is compiled out.
-    static_assert(epi_lds_bf16_elems<C, NA>() * 2 <= (int)sizeof(smem), "epilogue LDS");
+    static_assert(epi_lds_bf16_elems<C, NA>() * 2 <= kernel_smem_elems<C, T, NA, 1, NA>() * (int)sizeof(T), "epilogue LDS");
     for_each_row8_bf16<C, NA>(acc, reinterpret_cast<bf16_t*>(smem), alpha,
                               [&](int m, int n, const u32x4 (&p)[NA]) {
       if (m >= mv || n0 + n >= N) return;
@@ -1412,7 +1409,7 @@ __global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T
     });
     return;
   }
-  static_assert(epi_lds_floats<C, NA>() * 4 <= (int)sizeof(smem), "epilogue LDS");
+  static_assert(epi_lds_floats<C, NA>() * 4 <= kernel_smem_elems<C, T, NA, 1, NA>() * (int)sizeof(T), "epilogue LDS");
   if (groups.nsplit > 1) {  // fp32 partial tile of this chunk, [NA][nsplit][M][N]
     const int64_t MN = (int64_t)M * N;
     for_each_row8<C, NA>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
@@ -1436,6 +1433,41 @@ __global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T
       store8(o1 + o, r);
     }
   });
+}
+
+// One tile per block (block b is virtual block b), except when `slots` > 0
+// and the groups run whole per XCD (xcd_order flag set, as the device decided
+// from the expert counts): then the first `slots` blocks (a multiple of 8, at
+// most one per CU) are persistent and block b runs the virtual blocks b,
+// b + slots, ... below vblocks, each keeping the XCD of the block it stands
+// for; the other blocks leave at once.  A persistent workgroup issues its
+// next tile's first loads while the previous tile's output stores drain,
+// where a new workgroup could only start after them (a wave ends by waiting
+// for its stores): config 5 gate/up pair 6.57 -> 5.86 ms alone.  With every
+// expert's tiles dealt over all XCDs instead (skewed counts), tiles of very
+// different K would land unevenly on a static schedule, and the hardware's
+// dispatch balances them better.
+template <typename T, int NA, bool GROUPED>
+__global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
+                                               int64_t ldp, const T* __restrict__ Q, int64_t ldq,
+                                               KGroups groups, int M, int N, float alpha,
+                                               T* const* out0_tab, T* out0_one,
+                                               T* const* out1_tab, T* out1_one,
+                                               float* __restrict__ partial, int vblocks,
+                                               int slots) {
+  using C = WgradTiling<T, NA>;
+  __shared__ __align__(16) T smem[kernel_smem_elems<C, T, NA, 1, NA>()];
+  const bool persist = slots > 0 && groups.xcd_order && groups.xcd_order[groups.G];
+  if (!persist) {
+    wgrad_tile<T, NA, GROUPED>(smem, (int)blockIdx.x, P0, P1, ldp, Q, ldq, groups, M, N, alpha,
+                               out0_tab, out0_one, out1_tab, out1_one, partial);
+    return;
+  }
+  for (int vb = (int)blockIdx.x; blockIdx.x < (unsigned)slots && vb < vblocks; vb += slots) {
+    wgrad_tile<T, NA, GROUPED>(smem, vb, P0, P1, ldp, Q, ldq, groups, M, N, alpha, out0_tab,
+                               out0_one, out1_tab, out1_one, partial);
+    __syncthreads();  // the next tile's loads overwrite the epilogue's LDS
+  }
 }
 
 // out_x[i] = alpha * sum_s partial[x][s][i], s ascending; 8 elements per thread.

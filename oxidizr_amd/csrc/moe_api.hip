@@ -174,6 +174,9 @@ static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
 struct moe_plan {
   moe_config cfg;
   int device;
+  // workgroups of a persistent grouped weight-gradient launch: one per CU
+  // (its tilings hold one workgroup per CU), rounded down to whole XCD rounds
+  int wgrad_slots = 256;
   void* scratch_ptr = nullptr;  // device address of `scratch` on this plan's device
   // device pointer tables: 0 gate, 1 up, 2 down (weights); 3..5 their grads
   void** d_tab = nullptr;
@@ -313,6 +316,7 @@ struct moe_plan {
     L.dwn_b = g.take(blk ? 4 * (size_t)ceil_div(nrow, 256) * H : 0);
     // expert order of the gate/up weight gradient over the 8 XCDs and its flag
     L.xorder = g.take(4 * (size_t)(E + 1));
+
     L.total = f.off > g.off ? f.off : g.off;
     L.fwd_total = f.off;
     return L;
@@ -568,9 +572,9 @@ moe_status launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t l
                   sp.nsplit, need, partial_bytes);
   }
   const KGroups kg{nullptr, 1, T, sp.nsplit, sp.kchunk, 1, nullptr};
-  hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN)),
-                     dim3(C::THREADS), 0, s, P0, P1, ldp, Q,
-                     ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial);
+  const int grid = kgrouped_grid(sp.nsplit, M, N, C::BM, C::BN);
+  hipLaunchKernelGGL((k_wgrad<D, NA, false>), dim3(grid), dim3(C::THREADS), 0, s, P0, P1, ldp, Q,
+                     ldq, kg, M, N, alpha, nullptr, o0, nullptr, o1, partial, grid, 0);
   if (sp.nsplit > 1) {
     const int64_t MN = (int64_t)M * N;
     hipLaunchKernelGGL(k_splitk_reduce<D>, dim3(ceil_div(MN, 2048), NA), dim3(256), 0, s, partial,
@@ -988,7 +992,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     KGroups kgd = kg;
     kgd.col_walk = 1;
     hipLaunchKernelGGL((k_wgrad<D, 1, true>), dim3(grid), dim3(CS::THREADS), 0, ws2, dY, nullptr, (int64_t)H, A,
-                       (int64_t)I, kgd, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr);
+                       (int64_t)I, kgd, H, I, 1.0f, tdd, nullptr, nullptr, nullptr, nullptr, grid, 0);
     LAUNCH_CHECK();
   }
   {
@@ -1010,7 +1014,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     KGroups kgp = kg;
     kgp.xcd_order = xorder;
     hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(CW::THREADS), 0, ws2, dG, dU, (int64_t)I, xp,
-                       (int64_t)H, kgp, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr);
+                       (int64_t)H, kgp, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr, grid,
+                       std::min(grid, p->wgrad_slots));
     LAUNCH_CHECK();
   }
   {
@@ -1199,6 +1204,12 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
   if (!p) return fail(MOE_ERR_OOM, "host allocation of the plan failed");
   p->cfg = *cfg;
   p->device = device;
+  {
+    int ncu = 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess &&
+        ncu >= 8)
+      p->wgrad_slots = ncu / 8 * 8;
+  }
   // the static scratch of moe_forward_noalloc on this device (device current)
   if (resolve_scratch(device, &p->scratch_ptr) != MOE_OK) {
     delete p;
