@@ -1436,11 +1436,14 @@ MOE_DEV void wgrad_tile(T* smem, int blk, const T* __restrict__ P0, const T* __r
 }
 
 // One tile per block (block b is virtual block b), except when `slots` > 0
-// and the groups run whole per XCD (xcd_order flag set, as the device decided
-// from the expert counts): then the first `slots` blocks (a multiple of 8, at
-// most one per CU) are persistent and block b runs the virtual blocks b,
-// b + slots, ... below vblocks, each keeping the XCD of the block it stands
-// for; the other blocks leave at once.  A persistent workgroup issues its
+// and either the groups run whole per XCD (xcd_order flag set, as the device
+// decided from the expert counts) or the grid holds only `slots` blocks (the
+// host's expectation of that flag): then the first `slots` blocks (a
+// multiple of 8, at most one per CU) are persistent and block b runs the
+// virtual blocks b, b + slots, ... below vblocks, each keeping the XCD of the
+// block it stands for; the other blocks of a full grid leave at once.  Every
+// virtual block is computed once by one workgroup either way, so the results
+// are the same bits.  A persistent workgroup issues its
 // next tile's first loads while the previous tile's output stores drain,
 // where a new workgroup could only start after them (a wave ends by waiting
 // for its stores): config 5 gate/up pair 6.57 -> 5.86 ms alone.  With every
@@ -1457,7 +1460,11 @@ __global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T
                                                int slots) {
   using C = WgradTiling<T, NA>;
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, NA, 1, NA>()];
-  const bool persist = slots > 0 && groups.xcd_order && groups.xcd_order[groups.G];
+  // a grid of `slots` blocks (the host expected whole experts per XCD) runs
+  // persistent whatever the flag says; a full grid only when the flag is set
+  const bool reduced = (int)gridDim.x < vblocks;
+  const bool persist =
+      slots > 0 && (reduced || (groups.xcd_order && groups.xcd_order[groups.G]));
   if (!persist) {
     wgrad_tile<T, NA, GROUPED>(smem, (int)blockIdx.x, P0, P1, ldp, Q, ldq, groups, M, N, alpha,
                                out0_tab, out0_one, out1_tab, out1_one, partial);

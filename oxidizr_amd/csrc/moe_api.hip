@@ -185,6 +185,15 @@ struct moe_plan {
   // run (its event), so an upload never waits for the stream as a whole.
   static constexpr int kTabSlots = 16;
   void** h_tab = nullptr;
+  // The gate/up weight gradient's whole-experts-per-XCD flag of the last
+  // backward, read back without waiting (pinned copy + event): when it was
+  // set, the next backward launches only the persistent blocks (no blocks
+  // that would only exit).  A stale or unknown flag changes the grid, never
+  // the results.
+  int* h_xflag = nullptr;
+  hipEvent_t xflag_ev = nullptr;
+  bool xflag_pending = false;
+  int xflag = 0;
   hipEvent_t tab_ev[kTabSlots] = {};
   bool tab_ev_pending[kTabSlots] = {};
   int tab_next = 0;
@@ -979,9 +988,19 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   // whole experts per XCD for the gate/up weight gradient when the experts
   // split evenly over the XCDs (k_xcd_order decides on the device)
   int* xorder = E % 8 == 0 ? (int*)(ws + W.xorder) : nullptr;
+  if (p->xflag_pending && hipEventQuery(p->xflag_ev) == hipSuccess) {
+    p->xflag = *p->h_xflag;
+    p->xflag_pending = false;
+  }
+  const bool expect_whole = xorder && p->xflag == 1;
   if (xorder) {
     hipLaunchKernelGGL(k_xcd_order, dim3(1), dim3(1024), 0, ws2, counts, E, xorder);
     LAUNCH_CHECK();
+    if (!p->xflag_pending && p->h_xflag) {
+      HIP_TRY(hipMemcpyAsync(p->h_xflag, xorder + E, sizeof(int), hipMemcpyDeviceToHost, ws2));
+      HIP_TRY(hipEventRecord(p->xflag_ev, ws2));
+      p->xflag_pending = true;
+    }
   }
   {
     StageTimer tm(p, ws2, MOE_STAGE_DOWN_WGRAD);
@@ -1013,9 +1032,10 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     const int grid = kgrouped_grid(E, I, H, CW::BM, CW::BN);
     KGroups kgp = kg;
     kgp.xcd_order = xorder;
-    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(grid), dim3(CW::THREADS), 0, ws2, dG, dU, (int64_t)I, xp,
+    const int slots = std::min(grid, p->wgrad_slots);
+    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(expect_whole ? slots : grid), dim3(CW::THREADS), 0, ws2, dG, dU, (int64_t)I, xp,
                        (int64_t)H, kgp, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr, grid,
-                       std::min(grid, p->wgrad_slots));
+                       slots);
     LAUNCH_CHECK();
   }
   {
@@ -1232,6 +1252,8 @@ moe_status moe_plan_create(const moe_config* cfg, int device, moe_plan** out) {
   if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wfork, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wmid, hipEventDisableTiming);
   if (e == hipSuccess) e = hipEventCreateWithFlags(&p->wjoin, hipEventDisableTiming);
+  if (e == hipSuccess) e = hipHostMalloc((void**)&p->h_xflag, sizeof(int), hipHostMallocDefault);
+  if (e == hipSuccess) e = hipEventCreateWithFlags(&p->xflag_ev, hipEventDisableTiming);
   if (e != hipSuccess) {
     moe_plan_destroy(p);
     return fail(e == hipErrorOutOfMemory ? MOE_ERR_OOM : MOE_ERR_HIP, "plan set-up: %s",
@@ -1266,6 +1288,11 @@ moe_status moe_plan_destroy(moe_plan* p) {
   }
   if (p->d_tab) (void)hipFree(p->d_tab);
   if (p->h_tab) (void)hipHostFree(p->h_tab);
+  if (p->xflag_ev) {
+    if (p->xflag_pending) (void)hipEventSynchronize(p->xflag_ev);
+    (void)hipEventDestroy(p->xflag_ev);
+  }
+  if (p->h_xflag) (void)hipHostFree(p->h_xflag);
   delete p;
   return MOE_OK;
 }

@@ -41,9 +41,11 @@ class Case:
 
 
 def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x=None,
-            overlap=True, need_grad=True):
+            overlap=True, need_grad=True, backwards=1):
     """Forward (+ backward) on cuda:0. Returns a dict of numpy results.
-    need_grad=False: forward-only call without saved state (out, aux, z only)."""
+    need_grad=False: forward-only call without saved state (out, aux, z only).
+    backwards > 1: that many backward calls on the same plan and buffers, the
+    device synchronised between them (the results of the last one)."""
     dev = torch.device("cuda:0")
     p = case.p
     dt = case.tdtype
@@ -77,7 +79,11 @@ def gpu_run(case, d_aux=0.0, d_z=0.0, backward=True, nan_fill=True, dout=None, x
         has_grad = torch.full((case.E,), 7, dtype=torch.uint8, device=dev)
         da = torch.tensor(float(d_aux), device=dev)
         dz = torch.tensor(float(d_z), device=dev)
-        dx = plan.backward(t["x"], t["dout"], w, g, saved, d_aux=da, d_z=dz, has_grad=has_grad)
+        for i in range(backwards):
+            if i:
+                torch.cuda.synchronize()
+            dx = plan.backward(t["x"], t["dout"], w, g, saved, d_aux=da, d_z=dz,
+                               has_grad=has_grad)
         res.update({"dx": dx, "router": g_router, "router_bias": g_bias,
                     "gate": torch.stack(g_gate), "up": torch.stack(g_up),
                     "down": torch.stack(g_down), "has_grad": has_grad})

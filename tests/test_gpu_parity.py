@@ -237,6 +237,22 @@ def test_shared_stream_overlap_is_bitwise_serial(dtype, S, E):
         np.testing.assert_array_equal(np.nan_to_num(c[n]), np.nan_to_num(b[n]), err_msg=n)
 
 
+@pytest.mark.parametrize("skew", [0.0, 3.0])
+def test_repeated_backward_is_bitwise_first(skew):
+    # A plan's later backward calls may launch the gate/up weight gradient with
+    # only its persistent workgroups (when the previous call's expert counts
+    # ran whole experts per XCD); the first call launches the full grid.  Both
+    # compute every tile once: the same bits.  E = 16 balanced (whole experts
+    # per XCD) and skewed (tiles dealt over the XCDs).
+    bias = zipf_bias(16, s=1.2, beta=skew) if skew else None
+    case = Case(T=2048, H=128, E=16, k=2, I=64, S=0, dtype="bf16", w_std=0.05, seed=9,
+                bias=bias)
+    a = gpu_run(case, d_aux=0.01)
+    b = gpu_run(case, d_aux=0.01, backwards=3)
+    for n in ("dx", "router", "gate", "up", "down"):
+        np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_batch_invariance(dtype):
     # Routing is per token (reference tests/data_parallel.rs:333-347), and no
