@@ -1443,13 +1443,13 @@ MOE_DEV void wgrad_tile(T* smem, int blk, const T* __restrict__ P0, const T* __r
 // virtual blocks b, b + slots, ... below vblocks, each keeping the XCD of the
 // block it stands for; the other blocks of a full grid leave at once.  Every
 // virtual block is computed once by one workgroup either way, so the results
-// are the same bits.  A persistent workgroup issues its
-// next tile's first loads while the previous tile's output stores drain,
-// where a new workgroup could only start after them (a wave ends by waiting
-// for its stores): config 5 gate/up pair 6.57 -> 5.86 ms alone.  With every
-// expert's tiles dealt over all XCDs instead (skewed counts), tiles of very
-// different K would land unevenly on a static schedule, and the hardware's
-// dispatch balances them better.
+// are the same bits.  A persistent workgroup issues its next tile's first
+// loads while the previous tile's output stores drain, where a new workgroup
+// could only start after them (a wave ends by waiting for its stores):
+// config 5 gate/up pair 6.57 -> 5.86 ms alone.  With every expert's tiles
+// dealt over all XCDs instead (skewed counts), tiles of very different K
+// would land unevenly on a static schedule, and the hardware's dispatch
+// balances them better.
 template <typename T, int NA, bool GROUPED>
 __global__ __launch_bounds__((WgradTiling<T, NA>::THREADS)) void k_wgrad(const T* __restrict__ P0, const T* __restrict__ P1,
                                                int64_t ldp, const T* __restrict__ Q, int64_t ldq,
