@@ -125,6 +125,53 @@ def cpu_baseline(wl, seconds, threads):
             "kind": "port", "sample": sample, "seconds": round(t, 3)}
 
 
+def dropin_step(torch, cfg, dtype, dev, x, dout, router, gate, up, down, bias, shared, d_aux,
+                steps):
+    """The same forward + backward through the drop-in autograd module
+    (oxidizr_amd.moe.MoeLayer: torch autograd, fresh gradient tensors on every
+    call, parameters as separate tensors) on copies of the same weights and
+    inputs.  Reported beside the direct C-ABI step, which reuses its buffers."""
+    from oxidizr_amd.moe import MoeLayer
+    layer = MoeLayer(cfg, dtype=dtype, device=dev)
+    with torch.no_grad():
+        layer.router.gate.weight.copy_(router)
+        if bias is not None:
+            layer.router.bias.copy_(bias)
+        for e, ex in enumerate(layer.experts):
+            ex.gate_proj.weight.copy_(gate[e])
+            ex.up_proj.weight.copy_(up[e])
+            ex.down_proj.weight.copy_(down[e])
+        if shared:
+            for mod, t in zip((layer.shared_expert.gate_proj, layer.shared_expert.up_proj,
+                               layer.shared_expert.down_proj), shared):
+                mod.weight.copy_(t)
+    params = [prm for _, prm in layer.trainable_parameters()]
+    x3 = x.detach().reshape(1, *x.shape).clone().requires_grad_()
+    dout3 = dout.reshape(1, *dout.shape)
+    da = torch.tensor(float(d_aux), device=dev)
+    dz = torch.tensor(0.0, device=dev)
+
+    def one():
+        for prm in params:
+            prm.grad = None
+        x3.grad = None
+        out, aux, z = layer(x3)
+        torch.autograd.backward([out, aux, z], [dout3, da, dz])
+
+    for _ in range(2):
+        one()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        one()
+    torch.cuda.synchronize()
+    ms = (time.perf_counter() - t0) * 1e3 / steps
+    del layer, params, x3
+    torch.cuda.empty_cache()
+    return {"ms_per_step": round(ms, 4), "tokens_per_s": round(x.shape[0] / (ms * 1e-3), 1),
+            "steps": steps, "path": "oxidizr_amd.moe.MoeLayer forward + torch.autograd.backward"}
+
+
 def achievable_peaks():
     """Library bf16 GEMMs (hipBLASLt through torch.matmul) at a square shape and
     at the expert / shared-expert shapes of configs 2 and 5, and a plain 1 GiB
@@ -185,6 +232,9 @@ def main():
                     help="time the block's whole MoE sub-block (post_attention_layernorm "
                          "RMSNorm + MoE layer + residual add) through moe_block_forward / "
                          "moe_block_backward")
+    ap.add_argument("--dropin", choices=["on", "off"], default="on",
+                    help="also time the step through the drop-in autograd module "
+                         "(MoeLayer) on the same weights; reported as dropin_autograd")
     ap.add_argument("--recompute", action="store_true",
                     help="keep only the routing state between forward and backward and "
                          "recompute the expert activations in the backward (the plan's "
@@ -444,6 +494,9 @@ def main():
         "hbm_stages": hbm_stages,
         **extra,
     }
+    if wl.backward and not args.block and not args.recompute and args.dropin == "on":
+        res["dropin_autograd"] = dropin_step(torch, cfg, dtype, dev, x, dout, router, gate, up,
+                                             down, bias, shared, wl.alpha, min(args.steps, 10))
     if args.cpu_baseline == "on":
         try:
             threads = min(16, len(os.sched_getaffinity(0)))
