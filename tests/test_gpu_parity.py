@@ -107,6 +107,7 @@ FP32_CASES = [
     dict(T=150, H=64, E=10, k=6, I=32, S=16),       # 4 < k <= 8 (dx gathers sized for k <= 8)
     dict(T=130, H=3592, E=6, k=2, I=32, S=0, bias=True),  # router k-loop split in two chunks
     dict(T=200, H=64, E=1020, k=5, I=16, S=16),     # E not a multiple of 8, most experts empty
+    dict(T=100, H=64, E=4, k=1, I=32, S=0),         # top-1 routing
 ]
 
 
@@ -151,6 +152,9 @@ BF16_CASES = [
     dict(T=200, H=7176, E=136, k=4, I=32, S=16, bias=True),
     # the largest plan limits: E = 1024 experts, k = 16
     dict(T=300, H=64, E=1024, k=16, I=16, S=0),
+    # top-1 routing, fused router and tiled router
+    dict(T=300, H=128, E=8, k=1, I=64, S=32),
+    dict(T=260, H=128, E=72, k=1, I=64, S=0, bias=True),
 ]
 
 
