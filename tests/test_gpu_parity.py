@@ -155,6 +155,10 @@ BF16_CASES = [
     # top-1 routing, fused router and tiled router
     dict(T=300, H=128, E=8, k=1, I=64, S=32),
     dict(T=260, H=128, E=72, k=1, I=64, S=0, bias=True),
+    # just above the small-token paths (T = 65); the fused router over a wide
+    # H whose last 128-column chunk is partial (H = 3592 = 28 * 128 + 8)
+    dict(T=65, H=128, E=32, k=4, I=64, S=16),
+    dict(T=100, H=3592, E=16, k=2, I=32, S=0, bias=True),
 ]
 
 
