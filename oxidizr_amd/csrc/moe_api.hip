@@ -473,11 +473,13 @@ void launch_router_route(hipStream_t s, int T, const bf16_t* x, const bf16_t* wr
 
 // Routing (from logits already in saved, unless `routed`: the fused router
 // kernel has written the routing decisions too), losses' P statistics and
-// dispatch.
+// dispatch.  `defer_scatter` (with `routed`, T > kRouteSmallTokens): stop
+// after k_scan; the caller's gather writes perm and inv_perm
+// (k_scatter_gather16 from the group bases at W.gbase).
 template <typename D>
 moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
                        const SavedLayout& L, const WsLayout& W, SideJoin* pjoin,
-                       bool routed = false) {
+                       bool routed = false, bool defer_scatter = false) {
   const moe_config& c = p->cfg;
   const int T = (int)T64, E = c.num_experts, k = c.experts_per_tok;
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
@@ -535,8 +537,9 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
       int* gb = (int*)(ws + W.gbase);
       hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, (const int*)(ws + W.ghist), ng, E, gb,
                          counts, offsets, tprefix);
-      hipLaunchKernelGGL(k_scatter16, dim3(ceil_div(T, 256)), dim3(256), 0, s, idx, T, k, E, gb,
-                         perm, inv);
+      if (!defer_scatter)
+        hipLaunchKernelGGL(k_scatter16, dim3(ceil_div(T, 256)), dim3(256), 0, s, idx, T, k, E, gb,
+                           perm, inv);
     } else {
       const int nb = ceil_div(T, 256);
       int* bh = (int*)(ws + W.block_hist);
@@ -691,9 +694,12 @@ constexpr int kRouterSmallMaxExperts = 32;
 
 // Routed experts forward on stream s: gather X_perm, then G, U (when kept),
 // A and the per-assignment expert outputs Y.  `timed`: record the stages.
+// `gbase` (not null): the dispatch stopped after k_scan over the fused
+// router's 16-token groups, whose bases gbase holds, and the gather also
+// writes perm and inv_perm.
 template <typename D>
 moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State<D>& st,
-                      bool timed) {
+                      bool timed, const int* gbase = nullptr) {
   using CG = typename Tilings<D>::GateUp;
   using CB = typename Tilings<D>::Big;
   const moe_config& c = p->cfg;
@@ -707,10 +713,15 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   // gradient; otherwise the small-token kernel reads each assignment's token
   // row of x directly.
   const bool gather = !skinny || st.G != nullptr;
+  if (gbase && !gather) return fail(MOE_ERR_INVALID, "deferred scatter without a gather");
   if (gather) {
     StageTimer tm(p, s, stage(MOE_STAGE_GATHER));
-    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.inv, T, k, H,
-                       st.xp);
+    if (gbase)
+      hipLaunchKernelGGL(k_scatter_gather16<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.idx,
+                         T, k, E, H, gbase, st.perm, st.inv, st.xp);
+    else
+      hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.inv, T, k, H,
+                         st.xp);
     LAUNCH_CHECK();
   }
   const bf16_t* xsrc = (const bf16_t*)(gather ? st.xp : x);
@@ -841,7 +852,11 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused);
+  // the fused router's scatter runs inside the gather (T > kSkinnyMaxTokens:
+  // the routed forward gathers X_perm)
+  const bool defer = fused && T > kSkinnyMaxTokens;
+  static_assert(kSkinnyMaxTokens >= kRouteSmallTokens, "deferred scatter follows k_scan");
+  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused, defer);
   if (r != MOE_OK) return r;
   {
     // beside the dispatch when P is summed on the side stream (the kernel
@@ -853,7 +868,9 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
                        st.idx, st.lse, T, E, k, c.aux_switch_coef, c.aux_sqprob_coef, aux, z);
     LAUNCH_CHECK();
   }
-  if ((r = routed_fwd<D>(p, s, T, x, st, true)) != MOE_OK) return r;
+  if ((r = routed_fwd<D>(p, s, T, x, st, true, defer ? (const int*)(ws + W.gbase) : nullptr)) !=
+      MOE_OK)
+    return r;
   HIP_TRY(shared_join.join());
   {
     StageTimer tm(p, s, MOE_STAGE_COMBINE_FWD);
