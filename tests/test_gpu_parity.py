@@ -159,6 +159,9 @@ BF16_CASES = [
     # H whose last 128-column chunk is partial (H = 3592 = 28 * 128 + 8)
     dict(T=65, H=128, E=32, k=4, I=64, S=16),
     dict(T=100, H=3592, E=16, k=2, I=32, S=0, bias=True),
+    # the fused router's scatter-gather over rows of more than 512 16-byte
+    # vectors (H = 4104: a second chunk of one vector) and a ragged last group
+    dict(T=90, H=4104, E=8, k=3, I=32, S=0),
 ]
 
 
