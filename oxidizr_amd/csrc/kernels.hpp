@@ -1033,8 +1033,8 @@ __global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ 
   int rank = 0;
   for (int b = 0; b < nprev; b += 64) {
     const int v = b + lane < nprev ? prev[b + lane] : -1;
-    for (int j = 0; j < k; ++j) {
-      const int ej = __shfl(mine, j, 64);
+    for (int j = 0; j < k; ++j) {  // j is wave-uniform: read lane j directly
+      const int ej = __builtin_amdgcn_readlane(mine, j);
       const int n = __popcll(__ballot(v == ej));
       if (lane == j) rank += n;
     }
@@ -1048,11 +1048,11 @@ __global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ 
       inv_perm[(int64_t)t * k + lane] = q;
     }
   }
-  // b0 is wave-uniform, so every lane takes part in each broadcast
+  // b0 is wave-uniform, so the loop and its broadcasts are too
   for (int b0 = 0;;) {
     const int c0 = b0 + lane;
     for (int j = 0; j < k; ++j) {
-      const int q = __shfl(pos, j, 64);
+      const int q = __builtin_amdgcn_readlane(pos, j);
       if (q < 0) continue;
       T* dst = xp + (int64_t)q * H;
 #pragma unroll
