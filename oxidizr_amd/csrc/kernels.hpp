@@ -704,15 +704,21 @@ constexpr int kTilePrefixes = 3;
 constexpr int kNumTileBM = 2;
 __constant__ int kTileBM[kNumTileBM] = {128, 256};
 
-// Inclusive prefix sum across the 64 lanes of a wave.
-MOE_DEV int wave_incl_scan(int v) {
+// Inclusive prefix sums across the 64 lanes of a wave of N values at once:
+// each step issues the N shuffles before adding, so the N scans wait for one
+// LDS round trip per step instead of N.
+template <int N>
+MOE_DEV void wave_incl_scans(int (&v)[N]) {
   const int lane = threadIdx.x & 63;
 #pragma unroll
   for (int o = 1; o < 64; o <<= 1) {
-    const int t = __shfl_up(v, o, 64);
-    if (lane >= o) v += t;
+    int t[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) t[j] = __shfl_up(v[j], o, 64);
+#pragma unroll
+    for (int j = 0; j < N; ++j)
+      if (lane >= o) v[j] += t[j];
   }
-  return v;
 }
 
 // With cnt[e] (LDS, e < E <= 1024) in place, a block of 1024 threads writes
@@ -737,9 +743,12 @@ MOE_DEV void scan_counts(const int* cnt, int E, int* __restrict__ offsets,
            : kind == 1 ? c / bm + (r > bm / 2 ? 1 : 0)
                        : (r > 0 && r <= bm / 2 ? 1 : 0);
     }
-    incl[j] = wave_incl_scan(v[j]);
-    if (lane == 63) wsum[j * 16 + wave] = incl[j];
+    incl[j] = v[j];
   }
+  wave_incl_scans(incl);
+#pragma unroll
+  for (int j = 0; j < kScanCount; ++j)
+    if (lane == 63) wsum[j * 16 + wave] = incl[j];
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < kScanCount; ++j) {
