@@ -162,6 +162,9 @@ BF16_CASES = [
     # the fused router's scatter-gather over rows of more than 512 16-byte
     # vectors (H = 4104: a second chunk of one vector) and a ragged last group
     dict(T=90, H=4104, E=8, k=3, I=32, S=0),
+    # k = 16 on the fused router: a token's earlier group entries span four
+    # 64-entry ballot rounds of the scatter-gather
+    dict(T=120, H=64, E=24, k=16, I=16, S=0),
 ]
 
 
