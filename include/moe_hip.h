@@ -145,9 +145,14 @@ moe_status moe_forward(moe_plan* plan, void* stream, int64_t num_tokens, const v
  * MOE_ERR_UNSUPPORTED when num_tokens needs more scratch than that (the
  * forward regions of moe_workspace_bytes; decode-sized batches fit).  Every
  * call on one GPU shares that GPU's array, so calls that overlap on one GPU
- * (other streams, other plans, other threads) race; order them.  No
- * counterpart in the reference: for callers that cannot allocate device
- * memory (code under HIP graph capture, tight serving loops). */
+ * (other streams, other plans, other threads) race; order them.  Under HIP
+ * graph capture, call it once eagerly first with the same weight pointer
+ * tables: a table change while the stream captures is refused with
+ * MOE_ERR_UNSUPPORTED (the upload could not be replayed safely).  A captured
+ * call reads the plan's device pointer tables when it replays, so replay it
+ * only while the plan's last call used the same tables.  No counterpart in
+ * the reference: for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops). */
 moe_status moe_forward_noalloc(moe_plan* plan, void* stream, int64_t num_tokens, const void* x,
                                const moe_weights* w, void* out, float* aux_loss, float* z_loss);
 

@@ -566,39 +566,6 @@ __global__ __launch_bounds__(64 * kRouterWaves) __attribute__((amdgpu_waves_per_
   }
 }
 
-// Stable scatter over 16-token groups (the groups of k_router_route, whose
-// bases k_scan computed): the position of assignment (t, j) is the base of its
-// group and expert plus the number of earlier tokens of the group that chose
-// the same expert, read from a 16-bit token mask per (group, expert) built with
-// LDS atomic ORs (order-independent).  256 threads = 16 groups; E <= 64.
-__global__ __launch_bounds__(256) void k_scatter16(const int* __restrict__ idx, int Tn, int k,
-                                                   int E, const int* __restrict__ group_base,
-                                                   int* __restrict__ perm,
-                                                   int* __restrict__ inv_perm) {
-  __shared__ unsigned mask[16][kFusedRouterMaxExperts];
-  const int tid = threadIdx.x;
-  const int t = blockIdx.x * 256 + tid;
-  const int gl = tid >> 4, r = tid & 15;  // local group, rank of the token in it
-  for (int i = tid; i < 16 * kFusedRouterMaxExperts; i += 256) (&mask[0][0])[i] = 0u;
-  __syncthreads();
-  const bool valid = t < Tn;
-  int keys[16];
-  for (int j = 0; j < k; ++j) {
-    keys[j] = valid ? idx[(int64_t)t * k + j] : 0;
-    if (valid) atomicOr(&mask[gl][keys[j]], 1u << r);
-  }
-  __syncthreads();
-  if (!valid) return;
-  const int grp = t >> 4;
-  const unsigned below = (1u << r) - 1u;
-  for (int j = 0; j < k; ++j) {
-    const int e = keys[j];
-    const int pos = group_base[(int64_t)grp * E + e] + __popc(mask[gl][e] & below);
-    perm[pos] = t * k + j;
-    inv_perm[(int64_t)t * k + j] = pos;
-  }
-}
-
 // ------------------------------------------------------------------ column sums
 // part[rb, e] = sum over rows [rb*64, rb*64+64) of a[t, e], fixed order.
 __global__ __launch_bounds__(256) void k_colsum_partial(const float* __restrict__ a, int Tn, int E,
@@ -1005,13 +972,13 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
   }
 }
 
-// k_scatter16 and k_gather in one launch (after the fused router and k_scan
-// over its 16-token groups).  The wave of token t first issues its row's
+// The stable scatter and k_gather in one launch (after the fused router and
+// k_scan over its 16-token groups).  The wave of token t first issues its row's
 // loads, then finds where each of its k choices goes: the base of its group
 // and expert plus the number of earlier tokens of the group that chose the
 // same expert, counted from the group's idx entries before t's (64 at a time,
 // one ballot per choice; a token picks distinct experts, so each earlier
-// token counts at most once).  These are k_scatter16's positions.  Lane j < k
+// token counts at most once): expert ascending, then token ascending.  Lane j < k
 // writes perm and inv_perm for choice j; the row then goes to the k slots as
 // in k_gather.  A position outside [0, T k) (which valid routing never makes)
 // is skipped.

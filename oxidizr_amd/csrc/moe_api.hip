@@ -422,6 +422,16 @@ moe_status upload_tables(moe_plan* p, hipStream_t s, int first, const void* cons
       if (!tabs[i][e] || !aligned16(tabs[i][e]))
         return fail(MOE_ERR_INVALID, "expert %d pointer %d is NULL or not 16-byte aligned", e,
                     first + i);
+  // Under graph capture the copy below would be recorded as a node that
+  // replays whatever the staging slot holds later (the ring reuses it), and
+  // waiting for the slot's event is not allowed there: a capture must find
+  // the tables already on the device.
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  HIP_TRY(hipStreamIsCapturing(s, &cap));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(MOE_ERR_UNSUPPORTED,
+                "the expert pointer tables changed while the stream is capturing a graph; call "
+                "once with the same tables before capture");
   const int slot = p->tab_next;
   if (p->tab_ev_pending[slot]) {
     HIP_TRY(hipEventSynchronize(p->tab_ev[slot]));
@@ -473,13 +483,13 @@ void launch_router_route(hipStream_t s, int T, const bf16_t* x, const bf16_t* wr
 
 // Routing (from logits already in saved, unless `routed`: the fused router
 // kernel has written the routing decisions too), losses' P statistics and
-// dispatch.  `defer_scatter` (with `routed`, T > kRouteSmallTokens): stop
-// after k_scan; the caller's gather writes perm and inv_perm
-// (k_scatter_gather16 from the group bases at W.gbase).
+// dispatch.  With `routed` (T > kRouteSmallTokens) the dispatch stops after
+// k_scan: the caller's gather writes perm and inv_perm (k_scatter_gather16
+// from the group bases at W.gbase).
 template <typename D>
 moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
                        const SavedLayout& L, const WsLayout& W, SideJoin* pjoin,
-                       bool routed = false, bool defer_scatter = false) {
+                       bool routed = false) {
   const moe_config& c = p->cfg;
   const int T = (int)T64, E = c.num_experts, k = c.experts_per_tok;
   float* logits = (float*)(saved + L.f[MOE_SAVED_LOGITS]);
@@ -537,9 +547,6 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
       int* gb = (int*)(ws + W.gbase);
       hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, (const int*)(ws + W.ghist), ng, E, gb,
                          counts, offsets, tprefix);
-      if (!defer_scatter)
-        hipLaunchKernelGGL(k_scatter16, dim3(ceil_div(T, 256)), dim3(256), 0, s, idx, T, k, E, gb,
-                           perm, inv);
     } else {
       const int nb = ceil_div(T, 256);
       int* bh = (int*)(ws + W.block_hist);
@@ -852,11 +859,12 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  // the fused router's scatter runs inside the gather (T > kSkinnyMaxTokens:
-  // the routed forward gathers X_perm)
-  const bool defer = fused && T > kSkinnyMaxTokens;
-  static_assert(kSkinnyMaxTokens >= kRouteSmallTokens, "deferred scatter follows k_scan");
-  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused, defer);
+  // the fused router's scatter runs inside the gather: every fused call has
+  // T > kRouteSmallTokens = kSkinnyMaxTokens, so its routed forward gathers X_perm
+  static_assert(kSkinnyMaxTokens == kRouteSmallTokens,
+                "a fused-router batch is never a small-token batch: its gather writes perm");
+  const bool defer = fused;
+  moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused);
   if (r != MOE_OK) return r;
   {
     // beside the dispatch when P is summed on the side stream (the kernel

@@ -291,6 +291,22 @@ def test_config4_full_size_forward():
     assert rel(r["logits"], logits) < 1e-4
     assert rel(r["out"].float(), out) < 1e-2
     assert abs(float(r["aux"]) - float(aux)) < 1e-3 * abs(float(aux))
+    # The forward-only call (saved == NULL, need_grad = 0: the call bench.py
+    # times for this config) against the same reference, and bitwise equal to
+    # the training forward's output
+    cfg = MoeConfig(hidden_size=H, num_experts=E, experts_per_tok=k, intermediate_size=I,
+                    shared_expert_enabled=False)
+    plan = Plan(cfg, torch.bfloat16, dev)
+    w, _kw = plan.weights_struct(p["router"], list(p["gate"].unbind(0)), list(p["up"].unbind(0)),
+                                 list(p["down"].unbind(0)))
+    o2 = torch.full_like(p["x"], float("nan"))
+    a2 = torch.full((), float("nan"), device=dev)
+    z2 = torch.full((), float("nan"), device=dev)
+    plan.forward(p["x"], w, out=o2, aux=a2, z=z2, need_grad=False)
+    torch.cuda.synchronize()
+    assert rel(o2.float(), out) < 1e-2
+    assert torch.equal(o2, r["out"])
+    assert torch.equal(a2, r["aux"]) and torch.equal(z2, r["z"])
 
 
 def test_empty_batch_and_single_expert():

@@ -267,6 +267,64 @@ def test_repeated_backward_is_bitwise_first(skew):
         np.testing.assert_array_equal(np.nan_to_num(a[n]), np.nan_to_num(b[n]), err_msg=n)
 
 
+def _whole_experts_per_xcd(counts):
+    """Whether the gate/up weight gradient runs whole experts per XCD for these
+    counts: experts ranked by count (ties by index) dealt to the 8 XCDs in a
+    snake, and the busiest XCD within 8 % of the mean."""
+    E = len(counts)
+    rank = sorted(range(E), key=lambda e: (-int(counts[e]), e))
+    load = [0] * 8
+    for r, e in enumerate(rank):
+        x = r % 8 if (r // 8) % 2 == 0 else 7 - r % 8
+        load[x] += int(counts[e])
+    return 100 * 8 * max(load) <= 108 * sum(load)
+
+
+@pytest.mark.parametrize("shape", [dict(E=64, H=256, I=128), dict(E=16, H=1280, I=512)])
+def test_repeated_backward_alternating_routing_on_one_plan(shape):
+    # From its second backward a plan launches the gate/up weight gradient with
+    # only its persistent workgroups when the previous call's counts ran whole
+    # experts per XCD: here the grids (512 and 384 blocks) exceed the 256
+    # persistent ones.  Alternating balanced and skewed routing on one plan
+    # makes that expectation stale every other call (persistent over dealt
+    # tiles, then a full grid over whole experts); each call must still give
+    # the bits of a fresh plan's first backward.
+    E, H, I = shape["E"], shape["H"], shape["I"]
+    common = dict(T=2048, H=H, E=E, k=2, I=I, S=0, dtype="bf16", w_std=0.05, seed=21)
+    bal = Case(bias=np.zeros(E, np.float32), **common)
+    skw = Case(bias=zipf_bias(E, s=1.2, beta=3.0), **common)
+    ref = {"bal": gpu_run(bal, d_aux=0.01), "skw": gpu_run(skw, d_aux=0.01)}
+    assert _whole_experts_per_xcd(ref["bal"]["counts"]), "balanced case must run whole experts"
+    assert not _whole_experts_per_xcd(ref["skw"]["counts"]), "skewed case must deal tiles"
+    dev = torch.device("cuda:0")
+    dt = torch.bfloat16
+    t = {n: torch.tensor(v, device=dev).to(dt) for n, v in bal.p.items() if n != "router_bias"}
+    biases = {"bal": torch.tensor(bal.p["router_bias"], device=dev),
+              "skw": torch.tensor(skw.p["router_bias"], device=dev)}
+    plan = Plan(bal.cfg, dt, dev)
+    gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
+    g_router, g_bias = torch.empty_like(t["router"]), torch.empty(E, device=dev)
+    g_gate = [torch.empty_like(a) for a in gate]
+    g_up = [torch.empty_like(a) for a in up]
+    g_down = [torch.empty_like(a) for a in down]
+    g, _keep_g = plan.grads_struct(g_router, g_gate, g_up, g_down, g_bias, None)
+    da = torch.tensor(0.01, device=dev)
+    dz = torch.tensor(0.0, device=dev)
+    for call, name in enumerate(["bal", "skw", "bal", "skw", "skw", "bal", "bal"]):
+        for a in g_gate + g_up + g_down:
+            a.fill_(float("nan"))
+        w, _keep_w = plan.weights_struct(t["router"], gate, up, down, biases[name], None)
+        out, aux, z, saved = plan.forward(t["x"], w)
+        dx = plan.backward(t["x"], t["dout"], w, g, saved, d_aux=da, d_z=dz)
+        torch.cuda.synchronize()
+        print(f"call {call} {name}", flush=True)
+        got = {"dx": dx, "router": g_router, "gate": torch.stack(g_gate),
+               "up": torch.stack(g_up), "down": torch.stack(g_down)}
+        for n, v in got.items():
+            np.testing.assert_array_equal(np.nan_to_num(v.float().cpu().numpy()),
+                                          np.nan_to_num(ref[name][n]), err_msg=f"{call} {name} {n}")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 def test_batch_invariance(dtype):
     # Routing is per token (reference tests/data_parallel.rs:333-347), and no

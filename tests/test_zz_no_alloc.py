@@ -61,3 +61,62 @@ def test_forward_noalloc_refuses_oversized_batches():
     with pytest.raises(_lib.MoeError, match="static scratch") as e:
         plan.forward_noalloc(xb, w, torch.empty_like(xb), aux, z)
     assert e.value.status == 4
+
+
+def test_forward_noalloc_under_graph_capture():
+    """A captured moe_forward_noalloc replays the eager call's bits, every
+    replay, with eager calls of the plan between the replays; a capture whose
+    pointer tables differ from the plan's last call is refused on the host
+    (the table upload cannot be recorded safely) and leaves the plan usable."""
+    dev = torch.device("cuda:0")
+    case = Case(T=300, H=128, E=16, k=2, I=64, S=64, dtype="bf16", w_std=0.05, seed=53)
+    t = _tensors(case, dev)
+    plan = Plan(case.cfg, case.tdtype, dev)
+    gate, up, down = (list(t[n].unbind(0)) for n in ("gate", "up", "down"))
+    shared = (t["shared_gate"], t["shared_up"], t["shared_down"])
+    w, _keep = plan.weights_struct(t["router"], gate, up, down, None, shared)
+    x = t["x"].contiguous()
+    x_other = torch.flip(x, dims=[0]).contiguous()
+    ref_out, ref_aux, ref_z, _ = plan.forward(x, w, need_grad=False)
+    oth_out, _, _, _ = plan.forward(x_other, w, need_grad=False)
+    out, aux, z = torch.empty_like(x), torch.empty((), device=dev), torch.empty((), device=dev)
+    plan.forward_noalloc(x, w, out, aux, z)  # eager call first: the tables are on the device
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        plan.forward_noalloc(x, w, out, aux, z)
+    torch.cuda.synchronize()
+    eo = torch.empty_like(x)
+    for replay in range(3):
+        out.fill_(float("nan"))
+        aux.fill_(float("nan"))
+        z.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"replay {replay}", flush=True)
+        assert torch.equal(out, ref_out), replay
+        assert torch.equal(aux, ref_aux) and torch.equal(z, ref_z), replay
+        # eager work of the plan between replays (same tables, other tokens)
+        plan.forward_noalloc(x_other, w, eo, torch.empty((), device=dev),
+                             torch.empty((), device=dev))
+        torch.cuda.synchronize()
+        assert torch.equal(eo, oth_out), replay
+    # new weight tensors (same values) give new pointer tables: refused while capturing
+    gate2, up2, down2 = ([p.clone() for p in ps] for ps in (gate, up, down))
+    w2, _keep2 = plan.weights_struct(t["router"], gate2, up2, down2, None, shared)
+    out2 = torch.zeros_like(x)
+    graph2 = torch.cuda.CUDAGraph()
+    with pytest.raises(_lib.MoeError, match="capturing") as e:
+        with torch.cuda.graph(graph2):
+            out2.fill_(1.0)  # keeps the refused capture non-empty
+            plan.forward_noalloc(x, w2, out2, aux, z)
+    assert e.value.status == 4
+    torch.cuda.synchronize()
+    del graph2
+    # the plan still holds the first tables, and takes the new ones eagerly
+    o1 = torch.empty_like(x)
+    plan.forward_noalloc(x, w, o1, aux, z)
+    o2 = torch.empty_like(x)
+    plan.forward_noalloc(x, w2, o2, aux, z)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, ref_out) and torch.equal(o2, ref_out)
