@@ -99,6 +99,15 @@ moe_status moe_plan_destroy(moe_plan* plan);
  * limit of this implementation; callers that batch tokens query it). */
 moe_status moe_check_tokens(const moe_config* cfg, int64_t num_tokens);
 
+/* Device-free self-check of this implementation's workspace plan for a call
+ * over num_tokens tokens: every scratch region a launch uses, sized from the
+ * launch's own grid and split arithmetic, fits the region moe_workspace_bytes
+ * plans for it, and the regions of the forward (and of the backward) do not
+ * overlap.  MOE_OK, or the moe_check_tokens errors, or MOE_ERR_INVALID naming
+ * the region that does not fit.  No reference counterpart (a test of this
+ * implementation's sizing, callable without a GPU). */
+moe_status moe_workspace_check(const moe_config* cfg, int64_t num_tokens);
+
 /* Bytes of the caller-owned buffers for a call over num_tokens tokens. */
 size_t moe_saved_bytes(const moe_plan* plan, int64_t num_tokens);
 size_t moe_workspace_bytes(const moe_plan* plan, int64_t num_tokens);

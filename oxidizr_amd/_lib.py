@@ -22,6 +22,7 @@ EXPORTED = [
     "moe_saved_field_range", "moe_stage_name", "moe_plan_set_profiling", "moe_plan_stage_times",
     "moe_plan_set_shared_overlap", "moe_block_forward", "moe_block_backward",
     "moe_last_error", "moe_version", "moe_check_tokens", "moe_forward_noalloc",
+    "moe_workspace_check",
 ]
 NUM_STAGES = 20
 
@@ -80,6 +81,8 @@ def load():
     L.moe_plan_destroy.restype = i32
     L.moe_check_tokens.argtypes = [P(MoeConfigC), i64]
     L.moe_check_tokens.restype = i32
+    L.moe_workspace_check.argtypes = [P(MoeConfigC), i64]
+    L.moe_workspace_check.restype = i32
     L.moe_saved_bytes.argtypes = [_vp, i64]
     L.moe_saved_bytes.restype = sz
     L.moe_workspace_bytes.argtypes = [_vp, i64]

@@ -65,6 +65,16 @@ struct SavedLayout {
   size_t total;
 };
 
+// A named region of the workspace: phase 0 regions are the forward's scratch
+// (they never overlap each other), phase 1 the backward's (likewise); the two
+// phases alias, since a call runs one or the other.
+struct WsSpan {
+  const char* name;
+  size_t off, bytes;
+  int phase;
+};
+constexpr int kMaxWsSpans = 40;
+
 struct WsLayout {
   // forward
   size_t block_hist, block_base, colpart, ghist, gbase, gpart, rpart, sY, infer;
@@ -73,6 +83,8 @@ struct WsLayout {
       recomp, dxm, dwn, dwn_a, dwn_b, xorder;
   size_t total;
   size_t fwd_total;  // bytes a forward-only call touches (the forward regions)
+  WsSpan span[kMaxWsSpans];
+  int nspan = 0;
 };
 
 int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
@@ -94,6 +106,18 @@ bool fused_router(const moe_config& c, int64_t T) {
 int router_splits(const moe_config& c) {
   return c.hidden >= 3584 ? std::min(8, c.hidden / 1792) : 1;
 }
+// Which router GEMM a forward over T tokens runs.  The router GEMM has N = E:
+// up to kRouterSmallMaxExperts experts the 16 x 16 blocks of k_router_small
+// fill the GPU better than 128 x 128 tiles (config 2, E = 16: 31 -> 12 us; at
+// E = 64 the tiles are faster).
+constexpr int kRouterSmallMaxExperts = 32;
+enum class RouterPath { Fused, Small, Split, Tiled };
+RouterPath router_path(const moe_config& c, int64_t T) {
+  if (fused_router(c, T)) return RouterPath::Fused;
+  if (c.dtype == MOE_DTYPE_BF16 && (T <= kSkinnyMaxTokens || c.num_experts <= kRouterSmallMaxExperts))
+    return RouterPath::Small;
+  return router_splits(c) > 1 ? RouterPath::Split : RouterPath::Tiled;
+}
 template <class C>
 int router_kchunk(const moe_config& c) {
   const int n = router_splits(c);
@@ -105,6 +129,31 @@ int router_kchunk(const moe_config& c) {
 constexpr int64_t kMaxExtentBytes = int64_t(1) << 31;
 int ceil_div(int64_t a, int64_t b) { return (int)((a + b - 1) / b); }
 int round8(int v) { return (v + 7) / 8 * 8; }
+
+// Launch sizes that the workspace regions are planned for; the launches and
+// moe_workspace_check both take them from here.
+// Blocks of k_hist / k_scatter (256 tokens each).
+int hist_blocks(int64_t T) { return ceil_div(T, 256); }
+// 16-token groups of the fused router (its histograms, bases and sums).
+int route_groups(int64_t T) { return ceil_div(T, 16); }
+// Row blocks of the mean-probability column sums: 64 tokens each, or 64 of
+// the fused router's 16-token groups.
+int colsum_rows(int64_t T, bool routed) {
+  return routed ? ceil_div(route_groups(T), 64) : ceil_div(T, 64);
+}
+// Levels of the RMSNorm weight gradient's 16-ary reduction tree over nrow
+// partial rows: level(R, G, which) reduces R rows to G into buffer `which`
+// (0, 1, 0, ...); the last <= 16 rows are reduced into the output.
+template <class F>
+void norm_tree(int nrow, F&& level) {
+  int R = nrow, which = 0;
+  while (R > 16) {
+    const int G = ceil_div(R, 16);
+    level(R, G, which);
+    which ^= 1;
+    R = G;
+  }
+}
 
 // Split of a dense (all-token) weight gradient over K = tokens into fixed
 // chunks (each at least four k-tiles).  The count minimises a cost model in
@@ -137,6 +186,14 @@ SplitPlan plan_split(int M, int N, int K) {
   return {ceil_div(K, chunk), chunk};
 }
 
+// fp32 partial-tile bytes of one dense weight gradient (NA outputs of M x N
+// over T tokens) as launch_dense_wgrad splits it: 0 when it runs unsplit.
+template <typename D, int NA>
+size_t dense_wgrad_partial_bytes(int M, int N, int T) {
+  const SplitPlan sp = plan_split<WgradTiling<D, NA>>(M, N, T);
+  return sp.nsplit > 1 ? (size_t)NA * sp.nsplit * (size_t)M * N * 4 : 0;
+}
+
 // fp32 partial-tile bytes of the largest dense weight gradient of one backward:
 // the router's, or the shared expert's (they run concurrently, on separate
 // buffers).  Planned with the tilings the launches use (WgradTiling), so the
@@ -144,22 +201,11 @@ SplitPlan plan_split(int M, int N, int K) {
 // fit.
 template <typename D>
 size_t splitk_bytes(const moe_config& c, int64_t T, bool shared) {
-  using CB = WgradTiling<D, 1>;
-  using CW = WgradTiling<D, 2>;
   const int H = c.hidden, E = c.num_experts, S = c.shared_intermediate;
-  size_t most = 0;
-  auto need = [&](SplitPlan sp, int na, int M, int N) {
-    if (sp.nsplit > 1) {
-      const size_t b = (size_t)na * sp.nsplit * (size_t)M * N * 4;
-      if (b > most) most = b;
-    }
-  };
-  if (!shared) need(plan_split<CB>(E, H, (int)T), 1, E, H);
-  if (shared && S > 0) {
-    need(plan_split<CB>(H, S, (int)T), 1, H, S);
-    need(plan_split<CW>(S, H, (int)T), 2, S, H);
-  }
-  return most;
+  if (!shared) return dense_wgrad_partial_bytes<D, 1>(E, H, (int)T);
+  if (S == 0) return 0;
+  return std::max(dense_wgrad_partial_bytes<D, 1>(H, S, (int)T),
+                  dense_wgrad_partial_bytes<D, 2>(S, H, (int)T));
 }
 
 }  // namespace
@@ -277,54 +323,59 @@ struct moe_plan {
               I = cfg.intermediate, S = cfg.shared_intermediate;
     const int64_t TK = T * k;
     const size_t b = es();
-    const int nb = ceil_div(T, 256), nrb = ceil_div(T, 64);
+    const int nb = hist_blocks(T), nrb = colsum_rows(T, false);
     WsLayout L{};
-    Carve f;
-    L.block_hist = f.take(4 * (size_t)nb * E);
-    L.block_base = f.take(4 * (size_t)nb * E);
-    L.colpart = f.take(4 * (size_t)nrb * E);
+    Carve f, g;
+    auto put = [&](Carve& c, const char* name, size_t bytes) {
+      const size_t o = c.take(bytes);
+      if (L.nspan < kMaxWsSpans) L.span[L.nspan++] = {name, o, bytes, &c == &f ? 0 : 1};
+      return o;
+    };
+    L.block_hist = put(f, "block_hist", 4 * (size_t)nb * E);
+    L.block_base = put(f, "block_base", 4 * (size_t)nb * E);
+    L.colpart = put(f, "colpart", 4 * (size_t)nrb * E);
     // fused router: per 16-token group histograms, dispatch bases and
     // probability column sums
-    const size_t ng = fused_router(cfg, T) ? (size_t)ceil_div(T, 16) * E : 0;
-    L.ghist = f.take(4 * ng);
-    L.gbase = f.take(4 * ng);
-    L.gpart = f.take(4 * ng);
+    const size_t ng = fused_router(cfg, T) ? (size_t)route_groups(T) * E : 0;
+    L.ghist = put(f, "ghist", 4 * ng);
+    L.gbase = put(f, "gbase", 4 * ng);
+    L.gpart = put(f, "gpart", 4 * ng);
     // split router GEMM: fp32 partial logits per chunk of H
     const int rs = fused_router(cfg, T) ? 1 : router_splits(cfg);
-    L.rpart = f.take(rs > 1 ? 4 * (size_t)rs * T * E : 0);
-    L.sY = f.take(b * T * H);
+    L.rpart = put(f, "rpart", rs > 1 ? 4 * (size_t)rs * T * E : 0);
+    L.sY = put(f, "sY", b * T * H);
     // forward-only calls keep their routing and activations here, clear of
     // the forward scratch above (the backward regions below are unused then)
-    L.infer = f.take(saved_layout(T, Keep::Transient).total);
-    Carve g;
-    g.take(4 * (size_t)nrb * E);  // column partials of the router-bias gradient (offset 0)
-    L.dw = g.take(4 * TK);
-    L.dY = g.take(b * TK * H);
-    L.dG = g.take(b * TK * I);
-    L.dU = g.take(b * TK * I);
-    L.dXp = g.take(b * TK * H);
-    L.dlogits = g.take(4 * T * E);
-    L.dlogits_t = g.take(b * T * round8(E));
-    L.sdG = g.take(b * T * S);
-    L.sdU = g.take(b * T * S);
-    L.dxs = g.take(b * T * H);
+    L.infer = put(f, "infer", saved_layout(T, Keep::Transient).total);
+    // column partials of the router-bias gradient (offset 0)
+    put(g, "bias_colpart", 4 * (size_t)nrb * E);
+    L.dw = put(g, "dw", 4 * TK);
+    L.dY = put(g, "dY", b * TK * H);
+    L.dG = put(g, "dG", b * TK * I);
+    L.dU = put(g, "dU", b * TK * I);
+    L.dXp = put(g, "dXp", b * TK * H);
+    L.dlogits = put(g, "dlogits", 4 * T * E);
+    L.dlogits_t = put(g, "dlogits_t", b * T * round8(E));
+    L.sdG = put(g, "sdG", b * T * S);
+    L.sdU = put(g, "sdU", b * T * S);
+    L.dxs = put(g, "dxs", b * T * H);
     const bool f32 = cfg.dtype == MOE_DTYPE_F32;
-    L.splitk_router = g.take(f32 ? splitk_bytes<float>(cfg, T, false)
-                                 : splitk_bytes<bf16_t>(cfg, T, false));
-    L.splitk_shared = g.take(f32 ? splitk_bytes<float>(cfg, T, true)
-                                 : splitk_bytes<bf16_t>(cfg, T, true));
+    L.splitk_router = put(g, "splitk_router", f32 ? splitk_bytes<float>(cfg, T, false)
+                                                  : splitk_bytes<bf16_t>(cfg, T, false));
+    L.splitk_shared = put(g, "splitk_shared", f32 ? splitk_bytes<float>(cfg, T, true)
+                                                  : splitk_bytes<bf16_t>(cfg, T, true));
     // a recomputing backward rebuilds every activation here first
-    L.recomp = g.take(cfg.recompute_activations ? saved_layout(T, Keep::All).total : 0);
+    L.recomp = put(g, "recomp", cfg.recompute_activations ? saved_layout(T, Keep::All).total : 0);
     // fused block: the layer's input gradient, then the RMSNorm weight
     // gradient's partial rows and two levels of their fixed-order reduction
     const bool blk = cfg.fused_block != 0;
     const int nrow = ceil_div(T, kRmsRows);
-    L.dxm = g.take(blk ? b * T * H : 0);
-    L.dwn = g.take(blk ? 4 * (size_t)nrow * H : 0);
-    L.dwn_a = g.take(blk ? 4 * (size_t)ceil_div(nrow, 16) * H : 0);
-    L.dwn_b = g.take(blk ? 4 * (size_t)ceil_div(nrow, 256) * H : 0);
+    L.dxm = put(g, "dxm", blk ? b * T * H : 0);
+    L.dwn = put(g, "dwn", blk ? 4 * (size_t)nrow * H : 0);
+    L.dwn_a = put(g, "dwn_a", blk ? 4 * (size_t)ceil_div(nrow, 16) * H : 0);
+    L.dwn_b = put(g, "dwn_b", blk ? 4 * (size_t)ceil_div(nrow, 256) * H : 0);
     // expert order of the gate/up weight gradient over the 8 XCDs and its flag
-    L.xorder = g.take(4 * (size_t)(E + 1));
+    L.xorder = put(g, "xorder", 4 * (size_t)(E + 1));
 
     L.total = f.off > g.off ? f.off : g.off;
     L.fwd_total = f.off;
@@ -477,7 +528,7 @@ template <int NEB>
 void launch_router_route(hipStream_t s, int T, const bf16_t* x, const bf16_t* wr, const float* b,
                          int H, int E, int k, float tau, int norm, float* logits, float* probs,
                          float* lse, int* idx, float* w, int* ghist, float* gpart) {
-  hipLaunchKernelGGL((k_router_route<NEB>), dim3(ceil_div(T, 16)), dim3(64 * kRouterWaves), 0, s,
+  hipLaunchKernelGGL((k_router_route<NEB>), dim3(route_groups(T)), dim3(64 * kRouterWaves), 0, s,
                      x, wr, b, T, H, E, k, tau, norm, logits, probs, lse, idx, w, ghist, gpart);
 }
 
@@ -524,14 +575,14 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
     const hipStream_t ps = pjoin ? p->wgrad_stream(s) : s;
     if (pjoin) HIP_TRY(pjoin->fork(s, ps, p->wfork, p->wjoin));
     if (routed) {  // P from the fused router's per-group sums, in two fixed-order levels
-      const int ng = ceil_div(T, 16), nrb = ceil_div(ng, 64);
+      const int ng = route_groups(T), nrb = colsum_rows(T, true);
       float* part = (float*)(ws + W.colpart);
       hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps,
                          (const float*)(ws + W.gpart), ng, E, part);
       hipLaunchKernelGGL(k_colsum_final, dim3(ceil_div(E, 256)), dim3(256), 0, ps, part, nrb, E,
                          1.0f / (float)T, P);
     } else {
-      const int nrb = ceil_div(T, 64);
+      const int nrb = colsum_rows(T, false);
       float* part = (float*)(ws + W.colpart);
       hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, ps, probs,
                          T, E, part);
@@ -543,12 +594,12 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
   {
     StageTimer st(p, s, MOE_STAGE_DISPATCH);
     if (routed) {  // the fused router counted its 16-token groups' choices
-      const int ng = ceil_div(T, 16);
+      const int ng = route_groups(T);
       int* gb = (int*)(ws + W.gbase);
       hipLaunchKernelGGL(k_scan, dim3(1), dim3(1024), 0, s, (const int*)(ws + W.ghist), ng, E, gb,
                          counts, offsets, tprefix);
     } else {
-      const int nb = ceil_div(T, 256);
+      const int nb = hist_blocks(T);
       int* bh = (int*)(ws + W.block_hist);
       int* bb = (int*)(ws + W.block_base);
       hipLaunchKernelGGL(k_hist, dim3(nb), dim3(256), sizeof(int) * E, s, idx, T, k, E, bh);
@@ -583,7 +634,7 @@ moe_status launch_dense_wgrad(hipStream_t s, const D* P0, const D* P1, int64_t l
   using C = WgradTiling<D, NA>;
   const SplitPlan sp = plan_split<C>(M, N, T);
   if (sp.nsplit > 1) {
-    const size_t need = (size_t)NA * sp.nsplit * (size_t)M * N * 4;
+    const size_t need = dense_wgrad_partial_bytes<D, NA>(M, N, T);
     if (need > partial_bytes)
       return fail(MOE_ERR_UNSUPPORTED,
                   "weight-gradient split of %d chunks needs %zu bytes of partials, the workspace "
@@ -693,11 +744,6 @@ void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t 
   f(C{}, RowGroups{offsets, tp, tp + (E + 1), tp + 2 * (E + 1), E, (int)TK, half_last},
     [mt](int N) { return 8 * ceil_div(mt * ceil_div(N, C::BN), 8); });
 }
-
-// The router GEMM has N = E: up to this many experts the 16 x 16 blocks of
-// k_router_small fill the GPU better than 128 x 128 tiles (config 2, E = 16:
-// 31 -> 12 us; at E = 64 the tiles are faster).
-constexpr int kRouterSmallMaxExperts = 32;
 
 // Routed experts forward on stream s: gather X_perm, then G, U (when kept),
 // A and the per-assignment expert outputs Y.  `timed`: record the stages.
@@ -817,7 +863,8 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const bool fused = fused_router(c, T64);
   {
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
-    if (fused) {  // router GEMM, softmax, lse and top-k in one launch
+    const RouterPath rp = router_path(c, T64);
+    if (rp == RouterPath::Fused) {  // router GEMM, softmax, lse and top-k in one launch
       const bf16_t* xb = (const bf16_t*)x;
       const bf16_t* wrb = (const bf16_t*)w->router;
       const float* rbias = c.has_router_bias ? w->router_bias : nullptr;
@@ -831,12 +878,12 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
         launch_router_route<2>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
       else
         launch_router_route<4>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
-    } else if (std::is_same<D, bf16_t>::value && (T <= kSkinnyMaxTokens || E <= kRouterSmallMaxExperts)) {
+    } else if (rp == RouterPath::Small) {
       hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16) * ceil_div(T, 16)),
                          dim3(64 * kRouterWaves), 0, s, (const bf16_t*)x,
                          (const bf16_t*)w->router, c.has_router_bias ? w->router_bias : nullptr,
                          st.logits, T, H, E);
-    } else if (router_splits(c) > 1) {
+    } else if (rp == RouterPath::Split) {
       const int ns = router_splits(c);
       float* part = (float*)(ws + W.rpart);
       const int tiles = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
@@ -1088,7 +1135,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
                                                    splitk_bytes<D>(c, T, false));
     if (rr != MOE_OK) return rr;
     if (c.has_router_bias && g->router_bias) {
-      const int nrb = ceil_div(T, 64);
+      const int nrb = colsum_rows(T, false);
       float* part = (float*)(ws);  // column partials at workspace offset 0
       hipLaunchKernelGGL(k_colsum_partial, dim3(ceil_div(E, 64), nrb), dim3(256), 0, s, dl, T, E,
                          part);
@@ -1215,6 +1262,103 @@ moe_status check_tokens_cfg(const moe_config& c, int64_t T) {
 
 moe_status check_tokens(const moe_plan* p, int64_t T) { return check_tokens_cfg(p->cfg, T); }
 
+// The workspace plan of a call over T tokens against what its launches need,
+// without a device: every region a launch writes or reads (sized from the
+// same helpers the launches take their grids and splits from: hist_blocks,
+// route_groups, colsum_rows, router_path, dense_wgrad_partial_bytes,
+// norm_tree, the saved layouts) must fit the region ws_layout gives it, the
+// regions of one phase must not overlap, and every region must lie inside the
+// workspace (the forward's inside its forward part, which bounds the static
+// scratch of moe_forward_noalloc).
+template <typename D>
+moe_status check_workspace_plan(const moe_plan& p, int64_t T) {
+  const moe_config& c = p.cfg;
+  const int E = c.num_experts, k = c.experts_per_tok, H = c.hidden, I = c.intermediate,
+            S = c.shared_intermediate;
+  const int64_t TK = T * k;
+  const size_t b = sizeof(D);
+  const WsLayout W = p.ws_layout(T);
+  struct Need { const char* name; size_t bytes; };
+  Need need[kMaxWsSpans];
+  int n = 0;
+  auto add = [&](const char* name, size_t bytes) {
+    if (n < kMaxWsSpans) need[n++] = {name, bytes};
+  };
+  if (T > 0) {
+    const RouterPath rp = router_path(c, T);
+    const bool fused = rp == RouterPath::Fused;
+    if (T > kRouteSmallTokens) {
+      if (!fused) {
+        add("block_hist", 4 * (size_t)hist_blocks(T) * E);
+        add("block_base", 4 * (size_t)hist_blocks(T) * E);
+      } else {
+        add("ghist", 4 * (size_t)route_groups(T) * E);
+        add("gbase", 4 * (size_t)route_groups(T) * E);
+        add("gpart", 4 * (size_t)route_groups(T) * E);
+      }
+      add("colpart", 4 * (size_t)colsum_rows(T, fused) * E);
+    }
+    if (rp == RouterPath::Split) add("rpart", 4 * (size_t)router_splits(c) * T * E);
+    if (S > 0) add("sY", b * T * H);
+    add("infer", p.saved_layout(T, moe_plan::Keep::Transient).total);
+    if (c.has_router_bias) add("bias_colpart", 4 * (size_t)colsum_rows(T, false) * E);
+    add("dw", 4 * TK);
+    add("dY", b * TK * H);
+    add("dG", b * TK * I);
+    add("dU", b * TK * I);
+    add("dXp", b * TK * H);
+    add("dlogits", 4 * T * E);
+    add("dlogits_t", b * T * round8(E));
+    add("splitk_router", dense_wgrad_partial_bytes<D, 1>(E, H, (int)T));
+    if (S > 0) {
+      add("sdG", b * T * S);
+      add("sdU", b * T * S);
+      add("dxs", b * T * H);
+      add("splitk_shared", std::max(dense_wgrad_partial_bytes<D, 1>(H, S, (int)T),
+                                    dense_wgrad_partial_bytes<D, 2>(S, H, (int)T)));
+    }
+    if (c.recompute_activations) add("recomp", p.saved_layout(T, moe_plan::Keep::All).total);
+    if (c.fused_block) {
+      const int nrow = ceil_div(T, kRmsRows);
+      size_t rows[2] = {0, 0};
+      norm_tree(nrow, [&](int, int G, int which) {
+        rows[which] = std::max(rows[which], (size_t)G);
+      });
+      add("dxm", b * T * H);
+      add("dwn", 4 * (size_t)nrow * H);
+      add("dwn_a", 4 * rows[0] * H);
+      add("dwn_b", 4 * rows[1] * H);
+    }
+    if (E % 8 == 0) add("xorder", 4 * (size_t)(E + 1));
+  }
+  if (n >= kMaxWsSpans || W.nspan >= kMaxWsSpans)
+    return fail(MOE_ERR_INVALID, "workspace check: more regions than it records");
+  for (int i = 0; i < n; ++i) {
+    const WsSpan* sp = nullptr;
+    for (int j = 0; j < W.nspan; ++j)
+      if (strcmp(W.span[j].name, need[i].name) == 0) sp = &W.span[j];
+    if (!sp) return fail(MOE_ERR_INVALID, "workspace check: no region %s", need[i].name);
+    if (need[i].bytes > sp->bytes)
+      return fail(MOE_ERR_INVALID,
+                  "workspace check: T = %lld needs %zu bytes in region %s, which holds %zu",
+                  (long long)T, need[i].bytes, need[i].name, sp->bytes);
+  }
+  for (int i = 0; i < W.nspan; ++i) {
+    const WsSpan& a = W.span[i];
+    const size_t end = a.off + a.bytes;
+    if (end > W.total || (a.phase == 0 && end > W.fwd_total))
+      return fail(MOE_ERR_INVALID, "workspace check: region %s [%zu, %zu) outside the workspace",
+                  a.name, a.off, end);
+    for (int j = 0; j < W.nspan; ++j) {
+      const WsSpan& o = W.span[j];
+      if (j == i || o.phase != a.phase || a.bytes == 0 || o.bytes == 0) continue;
+      if (a.off < o.off + o.bytes && o.off < end)
+        return fail(MOE_ERR_INVALID, "workspace check: regions %s and %s overlap", a.name, o.name);
+    }
+  }
+  return MOE_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1328,6 +1472,16 @@ moe_status moe_check_tokens(const moe_config* cfg, int64_t T) {
   return check_tokens_cfg(*cfg, T);
 }
 
+moe_status moe_workspace_check(const moe_config* cfg, int64_t T) {
+  moe_status st = validate_config(cfg);
+  if (st != MOE_OK) return st;
+  if ((st = check_tokens_cfg(*cfg, T)) != MOE_OK) return st;
+  moe_plan plan;  // layout arithmetic only: no device resources
+  plan.cfg = *cfg;
+  return cfg->dtype == MOE_DTYPE_BF16 ? check_workspace_plan<bf16_t>(plan, T)
+                                      : check_workspace_plan<float>(plan, T);
+}
+
 size_t moe_saved_bytes(const moe_plan* p, int64_t T) {
   if (!p || T < 0) return 0;
   return p->kept_layout(T).total;
@@ -1382,15 +1536,13 @@ void launch_norm_bwd(moe_plan* p, hipStream_t s, int T, const D* dxm, const void
   else bwd(std::integral_constant<int, 4>());
   const float* in = part;
   float* bufs[2] = {(float*)(ws + W.dwn_a), (float*)(ws + W.dwn_b)};
-  int R = nrow, which = 0;
-  while (R > 16) {
-    const int G = ceil_div(R, 16);
-    hipLaunchKernelGGL(k_rowsum<float>, dim3(ceil_div(H, 2048), G), dim3(256), 0, s, in, R, H,
+  int R = nrow;
+  norm_tree(nrow, [&](int r, int G, int which) {
+    hipLaunchKernelGGL(k_rowsum<float>, dim3(ceil_div(H, 2048), G), dim3(256), 0, s, in, r, H,
                        16, bufs[which]);
     in = bufs[which];
-    which ^= 1;
     R = G;
-  }
+  });
   hipLaunchKernelGGL(k_rowsum<D>, dim3(ceil_div(H, 2048), 1), dim3(256), 0, s, in, R, H, R,
                      (D*)dnw);
 }

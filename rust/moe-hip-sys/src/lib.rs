@@ -114,6 +114,7 @@ pub mod ffi {
                                plan: *mut *mut MoePlan) -> MoeStatus;
         pub fn moe_plan_destroy(plan: *mut MoePlan) -> MoeStatus;
         pub fn moe_check_tokens(cfg: *const MoeConfigC, num_tokens: i64) -> MoeStatus;
+        pub fn moe_workspace_check(cfg: *const MoeConfigC, num_tokens: i64) -> MoeStatus;
         pub fn moe_saved_bytes(plan: *const MoePlan, num_tokens: i64) -> usize;
         pub fn moe_workspace_bytes(plan: *const MoePlan, num_tokens: i64) -> usize;
         pub fn moe_forward(plan: *mut MoePlan, stream: *mut c_void, num_tokens: i64,

@@ -151,3 +151,68 @@ def test_token_limit_follows_the_widest_operand():
     assert _check_tokens(32, 4, 2, 32, 0, 2**24 + 1) == 4  # above 2^24 tokens
     assert _check_tokens(64, 4, 2, 32, 0, -1) == 1
     assert _check_tokens(64, 4, 5, 32, 0, 8) == 1   # invalid config first
+
+
+def _cfg(H, E, k, I, S, bf16=True, **kw):
+    L = _lib.load()
+    c = _lib.MoeConfigC()
+    L.moe_config_default(ctypes.byref(c), H, E, k, I, S)
+    c.dtype = _lib.MOE_DTYPE_BF16 if bf16 else _lib.MOE_DTYPE_F32
+    for n, v in kw.items():
+        setattr(c, n, v)
+    return c
+
+
+# BASELINE configs 1-5 (H, E, k, I, S, bf16) and a few edge shapes
+_WS_CONFIGS = {
+    "cfg1": (384, 8, 2, 1024, 0, False), "cfg2": (2048, 16, 2, 1408, 2816, True),
+    "cfg3": (2048, 64, 6, 1408, 2816, True), "cfg4": (4096, 128, 8, 1536, 0, True),
+    "cfg5": (7168, 256, 8, 2048, 2048, True), "e1k1": (64, 1, 1, 32, 0, True),
+    "e1000": (128, 1000, 16, 64, 64, True), "f32wide": (2048, 64, 6, 1408, 2816, False),
+}
+
+
+def _token_limit(c):
+    """The largest token count moe_check_tokens accepts (T <= 2^24 and
+    T * max(H, I, S, 8 ceil(E / 8)) * b < 2^31)."""
+    b = 2 if c.dtype == _lib.MOE_DTYPE_BF16 else 4
+    wide = max(c.hidden, c.intermediate, c.shared_intermediate, (c.num_experts + 7) // 8 * 8)
+    return min(1 << 24, ((1 << 31) - 1) // (wide * b))
+
+
+@pytest.mark.parametrize("name", sorted(_WS_CONFIGS))
+@pytest.mark.parametrize("flags", [{}, {"recompute_activations": 1}, {"fused_block": 1},
+                                   {"has_router_bias": 1, "norm_topk_prob": 1}])
+def test_every_launch_fits_its_workspace_region(name, flags):
+    # The split-K partials of the dense weight gradients were once planned
+    # with one tiling and launched with another (the launch then wrote past its
+    # region); moe_workspace_check recomputes every launch's scratch need from
+    # the launches' own sizing and compares it with the plan, on the CPU.
+    H, E, k, I, S, bf16 = _WS_CONFIGS[name]
+    if flags.get("fused_block") and H > 8192:
+        pytest.skip("fused_block supports H <= 8192")
+    c = _cfg(H, E, k, I, S, bf16, **flags)
+    L = _lib.load()
+    limit = _token_limit(c)
+    assert L.moe_check_tokens(ctypes.byref(c), limit) == 0
+    assert L.moe_check_tokens(ctypes.byref(c), limit + 1) == 4
+    for T in sorted({0, 1, 16, 63, 64, 65, 255, 256, 257, 1024, 4097, 8192, 16384, 65536,
+                     limit}):
+        if T > limit:
+            continue
+        st = L.moe_workspace_check(ctypes.byref(c), T)
+        assert st == 0, (name, flags, T, L.moe_last_error().decode())
+    assert L.moe_workspace_check(ctypes.byref(c), limit + 1) == 4
+    assert L.moe_workspace_check(ctypes.byref(c), -1) == 1
+
+
+def test_workspace_check_refuses_bad_input():
+    # the config and token checks come before any layout arithmetic
+    L = _lib.load()
+    bad = _cfg(64, 4, 2, 32, 0, True)
+    bad.experts_per_tok = 9  # k > E: required_moe_dims refuses it
+    assert L.moe_workspace_check(ctypes.byref(bad), 64) == 1
+    assert b"experts_per_tok" in L.moe_last_error()
+    good = _cfg(64, 4, 2, 32, 0, True)
+    assert L.moe_workspace_check(ctypes.byref(good), -5) == 1
+    assert L.moe_workspace_check(ctypes.byref(good), (1 << 24) + 1) == 4
