@@ -213,57 +213,15 @@ def achievable_peaks():
     print(json.dumps(res), flush=True)
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
-    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run a plain device copy of MIB MiB (5 launches) and exit: the "
-                         "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
-    ap.add_argument("--achievable-peaks", action="store_true",
-                    help="only measure this box's achievable peaks (library bf16 GEMMs through "
-                         "torch.matmul = hipBLASLt, and a 1 GiB device copy) and exit")
-    ap.add_argument("--cpu-seconds", type=float, default=15.0)
-    ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--block", action="store_true",
-                    help="time the block's whole MoE sub-block (post_attention_layernorm "
-                         "RMSNorm + MoE layer + residual add) through moe_block_forward / "
-                         "moe_block_backward")
-    ap.add_argument("--dropin", choices=["on", "off"], default="on",
-                    help="also time the step through the drop-in autograd module "
-                         "(MoeLayer) on the same weights; reported as dropin_autograd")
-    ap.add_argument("--recompute", action="store_true",
-                    help="keep only the routing state between forward and backward and "
-                         "recompute the expert activations in the backward (the plan's "
-                         "recompute_activations; activation checkpointing)")
-    args = ap.parse_args()
-    if args.achievable_peaks:
-        achievable_peaks()
-        return
-    if args.copy_calibration:
-        import torch
-        n = args.copy_calibration * (1 << 20) // 4
-        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
-        dst = torch.empty_like(src)
-        for _ in range(5):
-            dst.copy_(src)
-        torch.cuda.synchronize()
-        print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
-                          "launches": 5}), flush=True)
-        return
-    if args.gpus != 1:
-        print("bench.py measures one MI355X: this build runs the MoE layer on a single GPU "
-              "(no expert parallelism); --gpus must be 1", file=sys.stderr)
-        sys.exit(2)
-
+def measure(args, config, steps, warmup, extras=True):
+    """One workload: warm-up steps, then `steps` timed steps, plus the
+    per-stage breakdown; returns the result dict (without cpu_baseline).
+    extras: also the drop-in autograd timing."""
     import torch
     from oxidizr_amd.moe import MoeConfig, Plan
     from oxidizr_amd.synth import WORKLOADS, skew_bias
 
-    wl = WORKLOADS[args.config]
+    wl = WORKLOADS[config]
     dev = torch.device("cuda:0")
     dtype = torch.float32 if wl.dtype == "f32" else torch.bfloat16
     T, H, E, k, I, S = wl.T, wl.H, wl.E, wl.k, wl.I, wl.S
@@ -353,7 +311,7 @@ def main():
     }
     peak_mfma = PEAK_FP32_TFLOPS if wl.dtype == "f32" else PEAK_BF16_TFLOPS
     ridge = peak_mfma * 1e12 / (PEAK_HBM_GBS * 1e9)   # flop per HBM byte
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         step()
     torch.cuda.synchronize()
     if wl.backward:
@@ -382,7 +340,7 @@ def main():
     plan.set_profiling([dominant])
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
@@ -398,8 +356,8 @@ def main():
     plan.set_profiling([])
     plan.set_shared_overlap(True)
 
-    ms_per_step = elapsed * 1e3 / args.steps
-    tok_s = T / (elapsed / args.steps)
+    ms_per_step = elapsed * 1e3 / steps
+    tok_s = T / (elapsed / steps)
     fwd_flops = 2 * T * H * E + 6 * TK * H * I + 6 * T * H * S
     total_flops = fwd_flops * (3 if wl.backward else 1)
     dom_avg_ms = dom_ms / max(dom_calls, 1)
@@ -411,8 +369,8 @@ def main():
                 "peak": PEAK_HBM_GBS, "unit": "GB/s"}
         roof["frac"] = round(roof["achieved"] / PEAK_HBM_GBS, 4)
         layer_bytes = (n_touched * 3 * H * I * b + E * H * b + 2 * T * H * b + T * E * 4 + TK * 8)
-        extra = {"layer_hbm_GBs": round(layer_bytes / (elapsed / args.steps) / 1e9, 1),
-                 "layer_hbm_frac": round(layer_bytes / (elapsed / args.steps) / 1e9 / PEAK_HBM_GBS, 4)}
+        extra = {"layer_hbm_GBs": round(layer_bytes / (elapsed / steps) / 1e9, 1),
+                 "layer_hbm_frac": round(layer_bytes / (elapsed / steps) / 1e9 / PEAK_HBM_GBS, 4)}
         roof["kernel"] = (f"k_skinny_fwd<true, false> (gate/up weight stream + SwiGLU), "
                           f"{dom_avg_ms:.4f} ms/launch")
     else:
@@ -471,8 +429,8 @@ def main():
     res = {
         "metric": "MoE layer fwd+bwd tokens/sec on 1 MI355X; % bf16 MFMA peak; % HBM peak"
                   if wl.backward else "MoE layer fwd tokens/sec on 1 MI355X; % HBM peak",
-        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "value": round(tok_s, 1), "unit": "tokens/s", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16" if wl.dtype == "bf16" else "f32",
         "data": "synthetic (seeded N(0,1) tokens, N(0,std) random-init weights)",
@@ -487,16 +445,89 @@ def main():
                    "saved_MB_per_layer": round(plan.saved_bytes(T) / 1e6, 1),
                    "workspace_MB": round(plan.workspace_bytes(T) / 1e6, 1)},
         "roofline": roof,
-        "layer_tflops": round(total_flops / (elapsed / args.steps) / 1e12, 1),
-        "layer_mfma_frac": round(total_flops / (elapsed / args.steps) / 1e12 / peak, 4),
+        "layer_tflops": round(total_flops / (elapsed / steps) / 1e12, 1),
+        "layer_mfma_frac": round(total_flops / (elapsed / steps) / 1e12 / peak, 4),
         "gemm_tflops": round(total_flops / (gemm_ms * 1e-3) / 1e12, 1) if gemm_ms else None,
         "stages_ms": {n: round(v, 4) for n, v in stages.items()},
         "hbm_stages": hbm_stages,
         **extra,
     }
-    if wl.backward and not args.block and not args.recompute and args.dropin == "on":
+    if extras and wl.backward and not args.block and not args.recompute and args.dropin == "on":
         res["dropin_autograd"] = dropin_step(torch, cfg, dtype, dev, x, dout, router, gate, up,
-                                             down, bias, shared, wl.alpha, min(args.steps, 10))
+                                             down, bias, shared, wl.alpha, min(steps, 10))
+    del plan, saved
+    return res, wl
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=5, choices=[1, 2, 3, 4, 5])
+    ap.add_argument("--cpu-baseline", choices=["on", "off"], default="on")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain device copy of MIB MiB (5 launches) and exit: the "
+                         "reference kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
+    ap.add_argument("--achievable-peaks", action="store_true",
+                    help="only measure this box's achievable peaks (library bf16 GEMMs through "
+                         "torch.matmul = hipBLASLt, and a 1 GiB device copy) and exit")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--block", action="store_true",
+                    help="time the block's whole MoE sub-block (post_attention_layernorm "
+                         "RMSNorm + MoE layer + residual add) through moe_block_forward / "
+                         "moe_block_backward")
+    ap.add_argument("--dropin", choices=["on", "off"], default="on",
+                    help="also time the step through the drop-in autograd module "
+                         "(MoeLayer) on the same weights; reported as dropin_autograd")
+    ap.add_argument("--per-config", choices=["on", "off"], default="on",
+                    help="after the config-5 line, also run configs 2, 3 and 4 for 10 steps "
+                         "each and report them under per_config")
+    ap.add_argument("--recompute", action="store_true",
+                    help="keep only the routing state between forward and backward and "
+                         "recompute the expert activations in the backward (the plan's "
+                         "recompute_activations; activation checkpointing)")
+    args = ap.parse_args()
+    if args.achievable_peaks:
+        achievable_peaks()
+        return
+    if args.copy_calibration:
+        import torch
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes_read": n * 4, "bytes_written": n * 4,
+                          "launches": 5}), flush=True)
+        return
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: this build runs the MoE layer on a single GPU "
+              "(no expert parallelism); --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+
+    res, wl = measure(args, args.config, args.steps, args.warmup)
+    if args.per_config == "on" and args.config == 5 and not args.block and not args.recompute:
+        # the other north-star targets (configs 2, 3: layer MFMA fraction; 4:
+        # small-token forward against HBM), a few steps each, after the headline
+        import torch
+        torch.cuda.empty_cache()
+        res["per_config"] = {}
+        for c in (2, 3, 4):
+            sub, swl = measure(args, c, 10, 3, extras=False)
+            torch.cuda.empty_cache()
+            entry = {"ms_per_step": sub["ms_per_step"], "tokens_per_s": sub["value"],
+                     "steps": sub["steps"], "roofline": sub["roofline"]}
+            if swl.backward:
+                entry.update(layer_tflops=sub["layer_tflops"],
+                             layer_mfma_frac=sub["layer_mfma_frac"],
+                             alone_stage_ms=sub.get("alone_stage_ms"))
+            else:
+                entry.update(layer_hbm_GBs=sub["layer_hbm_GBs"],
+                             layer_hbm_frac=sub["layer_hbm_frac"])
+            res["per_config"][swl.name] = entry
     if args.cpu_baseline == "on":
         try:
             threads = min(16, len(os.sched_getaffinity(0)))
