@@ -566,6 +566,60 @@ __global__ __launch_bounds__(64 * kRouterWaves) __attribute__((amdgpu_waves_per_
   }
 }
 
+// The split router GEMM's chunks added in order, then the bias (the
+// arithmetic of k_router_reduce), and the routing of one 16-token group as in
+// k_router_route: one wave per token (route_row from the logits row in LDS),
+// the group's expert histogram and probability column sums for k_scan and the
+// column-sum kernels (as k_router_route writes them).  E <= 64 EPL.
+template <int EPL>
+__global__ __launch_bounds__(1024) void k_reduce_route(
+    const float* __restrict__ partial, int nsplit, int Tn, int E, int k, float tau, int norm,
+    const float* __restrict__ bias, float* __restrict__ logits, float* __restrict__ probs,
+    float* __restrict__ lse, int* __restrict__ idx, float* __restrict__ w,
+    int* __restrict__ group_hist, float* __restrict__ prob_part) {
+  __shared__ float lg[16][64 * EPL];
+  __shared__ float pl[16][64 * EPL];
+  __shared__ int hist[64 * EPL];
+  const int t0 = blockIdx.x * 16;
+  const int wave = uni(threadIdx.x >> 6), lane = threadIdx.x & 63;
+  const int ntok = min(16, Tn - t0);
+  const int64_t TE = (int64_t)Tn * E;
+  if (threadIdx.x < 64 * EPL) hist[threadIdx.x] = 0;
+  if (wave < ntok) {
+    const int t = t0 + wave;
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+      const int e = lane + 64 * i;
+      if (e < E) {
+        const int64_t o = (int64_t)t * E + e;
+        float v = partial[o];
+        for (int sp = 1; sp < nsplit; ++sp) v += partial[(int64_t)sp * TE + o];
+        v = v + (bias ? bias[e] : 0.0f);
+        lg[wave][e] = v;
+        logits[o] = v;
+      }
+    }
+  }
+  __syncthreads();
+  if (wave < ntok) {
+    const int t = t0 + wave;
+    float pr[EPL];
+    int sel;
+    route_row<EPL>(&lg[wave][0], t, E, k, tau, norm, probs, lse, idx, w, pr, sel);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) pl[wave][lane + 64 * i] = pr[i];
+    if (lane < k) atomicAdd(&hist[sel], 1);
+  }
+  __syncthreads();
+  const int b = blockIdx.x;
+  for (int e = threadIdx.x; e < E; e += 1024) {
+    group_hist[(int64_t)b * E + e] = hist[e];
+    float sum = 0.0f;
+    for (int i = 0; i < ntok; ++i) sum += pl[i][e];
+    prob_part[(int64_t)b * E + e] = sum;
+  }
+}
+
 // ------------------------------------------------------------------ column sums
 // part[rb, e] = sum over rows [rb*64, rb*64+64) of a[t, e], fixed order.
 __global__ __launch_bounds__(256) void k_colsum_partial(const float* __restrict__ a, int Tn, int E,

@@ -118,6 +118,18 @@ RouterPath router_path(const moe_config& c, int64_t T) {
     return RouterPath::Small;
   return router_splits(c) > 1 ? RouterPath::Split : RouterPath::Tiled;
 }
+// The split router GEMM's partials are summed and routed by k_reduce_route
+// (routing of one 16-token group per workgroup) for up to this many experts.
+constexpr int kReduceRouteMaxExperts = 256;
+// Whether the router path also routes the tokens and writes the 16-token
+// groups' histograms and probability sums (the fused router, or the split
+// router GEMM with k_reduce_route): the dispatch then scans those groups and
+// the gather writes the permutation.  Always T > kRouteSmallTokens.
+bool group_routing(const moe_config& c, int64_t T) {
+  const RouterPath rp = router_path(c, T);
+  return rp == RouterPath::Fused || (rp == RouterPath::Split && T > kRouteSmallTokens &&
+                                     c.num_experts <= kReduceRouteMaxExperts);
+}
 template <class C>
 int router_kchunk(const moe_config& c) {
   const int n = router_splits(c);
@@ -336,12 +348,12 @@ struct moe_plan {
     L.colpart = put(f, "colpart", 4 * (size_t)nrb * E);
     // fused router: per 16-token group histograms, dispatch bases and
     // probability column sums
-    const size_t ng = fused_router(cfg, T) ? (size_t)route_groups(T) * E : 0;
+    const size_t ng = group_routing(cfg, T) ? (size_t)route_groups(T) * E : 0;
     L.ghist = put(f, "ghist", 4 * ng);
     L.gbase = put(f, "gbase", 4 * ng);
     L.gpart = put(f, "gpart", 4 * ng);
     // split router GEMM: fp32 partial logits per chunk of H
-    const int rs = fused_router(cfg, T) ? 1 : router_splits(cfg);
+    const int rs = router_path(cfg, T) == RouterPath::Split ? router_splits(cfg) : 1;
     L.rpart = put(f, "rpart", rs > 1 ? 4 * (size_t)rs * T * E : 0);
     L.sY = put(f, "sY", b * T * H);
     // forward-only calls keep their routing and activations here, clear of
@@ -860,7 +872,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     shared_fwd<D>(p, ss, T, x, w, st.sG, st.sU, st.sA, sY);
     LAUNCH_CHECK();
   }
-  const bool fused = fused_router(c, T64);
+  const bool fused = group_routing(c, T64);
   {
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
     const RouterPath rp = router_path(c, T64);
@@ -889,9 +901,26 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
       const int tiles = ceil_div(T, CR::BM) * ceil_div(E, CR::BN);
       hipLaunchKernelGGL((k_router_logits_split<D, CR>), dim3(tiles * ns), dim3(CR::THREADS), 0, s,
                          x, (const D*)w->router, part, T, H, E, router_kchunk<CR>(c));
-      const int64_t TE = (int64_t)T * E;
-      hipLaunchKernelGGL(k_router_reduce, dim3(ceil_div(TE, 256)), dim3(256), 0, s, part, ns, TE, E,
-                         c.has_router_bias ? w->router_bias : nullptr, st.logits);
+      const float* rbias = c.has_router_bias ? w->router_bias : nullptr;
+      if (fused) {  // the chunks' sum, the routing and the group statistics in one launch
+        int* gh = (int*)(ws + W.ghist);
+        float* gp = (float*)(ws + W.gpart);
+        const float tau = c.router_temperature;
+        const int nt = c.norm_topk_prob;
+        auto go = [&](auto epl) {
+          constexpr int EPL = decltype(epl)::value;
+          hipLaunchKernelGGL((k_reduce_route<EPL>), dim3(route_groups(T)), dim3(1024), 0, s, part,
+                             ns, T, E, k, tau, nt, rbias, st.logits, st.probs, st.lse, st.idx,
+                             st.w, gh, gp);
+        };
+        if (E <= 64) go(std::integral_constant<int, 1>());
+        else if (E <= 128) go(std::integral_constant<int, 2>());
+        else go(std::integral_constant<int, 4>());
+      } else {
+        const int64_t TE = (int64_t)T * E;
+        hipLaunchKernelGGL(k_router_reduce, dim3(ceil_div(TE, 256)), dim3(256), 0, s, part, ns,
+                           TE, E, rbias, st.logits);
+      }
     } else {
       using CRN = typename Tilings<D>::RouterNarrow;
       const float* rbias = c.has_router_bias ? w->router_bias : nullptr;
@@ -1286,7 +1315,7 @@ moe_status check_workspace_plan(const moe_plan& p, int64_t T) {
   };
   if (T > 0) {
     const RouterPath rp = router_path(c, T);
-    const bool fused = rp == RouterPath::Fused;
+    const bool fused = group_routing(c, T);
     if (T > kRouteSmallTokens) {
       if (!fused) {
         add("block_hist", 4 * (size_t)hist_blocks(T) * E);
