@@ -653,11 +653,17 @@ MOE_DEV void for_each_frag(const f32x16 (&acc)[NACC][C::TN][C::TM], F&& f) {
       }
 }
 
-// LDS floats the row epilogue needs: every wave stages NACC blocks of WM x 32
-// accumulators, rows padded to 36 floats.
-template <class C, int NACC>
-constexpr int epi_lds_floats() { return C::NW * NACC * C::WM * 36; }
 constexpr int kLdsBytes = 160 * 1024;  // LDS one workgroup may hold on gfx950
+// Rows of a wave's block the row epilogue stages at once: all WM rows, or one
+// 32-row MFMA block at a time when the whole blocks of every wave would
+// outgrow the LDS (the 96-row wave blocks of a 192-row tile with two
+// accumulator sets).
+template <class C, int NACC>
+constexpr int epi_rows() { return C::NW * NACC * C::WM * 36 * 4 <= kLdsBytes ? C::WM : 32; }
+// LDS floats the row epilogue needs: every wave stages NACC blocks of
+// epi_rows x 32 accumulators, rows padded to 36 floats.
+template <class C, int NACC>
+constexpr int epi_lds_floats() { return C::NW * NACC * epi_rows<C, NACC>() * 36; }
 
 // LDS elements of a kernel whose main loop (NA A / NB B operands) is followed
 // by the row epilogue over NACC accumulator sets in the same buffer.
@@ -670,8 +676,8 @@ constexpr int kernel_smem_elems() {
 
 // Row epilogue: calls f(m_local, n_local, v, q) with v[x][i] = acc[x] at
 // (m_local, n_local + i) for i < 8, n_local a multiple of 8.  The accumulators
-// of one 32-column block are first written to a wave-private LDS region and
-// read back as rows, so the caller's element-wise work runs on 8 consecutive
+// of one 32-column block (epi_rows rows of it at a time) are first written to
+// a wave-private LDS region and read back as rows, so the caller's element-wise work runs on 8 consecutive
 // outputs per lane (16-byte bf16 stores) and only one block's accumulators is
 // in VGPRs at a time.  The LDS must no longer be in use by the main loop (it
 // ends with a barrier); regions are wave-private, so no barrier is needed.
@@ -685,52 +691,60 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
   static_assert(C::WM % 16 == 0, "rows are visited 16 at a time");
   constexpr int P = 36;  // padded row pitch (floats)
   constexpr int NQ = NPRE > 0 ? NPRE : 1;
-  constexpr int RG = C::WM / 16;  // row groups of a block
+  constexpr int SR = epi_rows<C, NACC>();  // rows staged per pass
+  constexpr int NSP = C::WM / SR;          // passes per 32-column block
+  constexpr int RG = SR / 16;              // row groups of a pass
+  static_assert(C::WM % SR == 0 && SR % 32 == 0, "whole MFMA blocks per pass");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
-  float* reg = lds + wave * NACC * C::WM * P;
+  float* reg = lds + wave * NACC * SR * P;
 #pragma unroll
   for (int tn = 0; tn < C::TN; ++tn) {  // unrolled: acc is indexed by constants only
-    u32x4 q[RG][NQ];
-    if constexpr (NPRE > 0) {
 #pragma unroll
-      for (int g = 0; g < RG; ++g)
-        pre(wm * C::WM + g * 16 + (lane >> 2), wn * C::WN + tn * 32 + (lane & 3) * 8, q[g]);
-    }
+    for (int sp = 0; sp < NSP; ++sp) {
+      const int r0 = wm * C::WM + sp * SR;  // first row of this pass
+      u32x4 q[RG][NQ];
+      if constexpr (NPRE > 0) {
 #pragma unroll
-    for (int x = 0; x < NACC; ++x)
-#pragma unroll
-      for (int tm = 0; tm < C::TM; ++tm)
-#pragma unroll
-        for (int qq = 0; qq < 4; ++qq) {
-          const int row = tm * 32 + (lane & 31);
-          const int col = 8 * qq + 4 * (lane >> 5);
-          *reinterpret_cast<f32x4*>(reg + (x * C::WM + row) * P + col) =
-              f32x4{acc[x][tn][tm][4 * qq], acc[x][tn][tm][4 * qq + 1],
-                    acc[x][tn][tm][4 * qq + 2], acc[x][tn][tm][4 * qq + 3]};
-        }
-    __builtin_amdgcn_sched_barrier(0);
-    auto visit = [&](int g) {
-      const int row = g * 16 + (lane >> 2);
-      const int col = (lane & 3) * 8;
-      float v[NACC][8];
-#pragma unroll
-      for (int x = 0; x < NACC; ++x) {
-        const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + (x * C::WM + row) * P + col);
-        const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + (x * C::WM + row) * P + col + 4);
-        v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
-        v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
+        for (int g = 0; g < RG; ++g)
+          pre(r0 + g * 16 + (lane >> 2), wn * C::WN + tn * 32 + (lane & 3) * 8, q[g]);
       }
-      f(wm * C::WM + row, wn * C::WN + tn * 32 + col, v, q[g]);
-    };
-    if constexpr (NPRE > 0) {
 #pragma unroll
-      for (int g = 0; g < RG; ++g) visit(g);  // q[g] needs constant indices
-    } else {
+      for (int x = 0; x < NACC; ++x)
+#pragma unroll
+        for (int tl = 0; tl < SR / 32; ++tl)
+#pragma unroll
+          for (int qq = 0; qq < 4; ++qq) {
+            const int tm = sp * (SR / 32) + tl;
+            const int row = tl * 32 + (lane & 31);
+            const int col = 8 * qq + 4 * (lane >> 5);
+            *reinterpret_cast<f32x4*>(reg + (x * SR + row) * P + col) =
+                f32x4{acc[x][tn][tm][4 * qq], acc[x][tn][tm][4 * qq + 1],
+                      acc[x][tn][tm][4 * qq + 2], acc[x][tn][tm][4 * qq + 3]};
+          }
+      __builtin_amdgcn_sched_barrier(0);
+      auto visit = [&](int g) {
+        const int row = g * 16 + (lane >> 2);
+        const int col = (lane & 3) * 8;
+        float v[NACC][8];
+#pragma unroll
+        for (int x = 0; x < NACC; ++x) {
+          const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col);
+          const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col + 4);
+          v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
+          v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
+        }
+        f(r0 + row, wn * C::WN + tn * 32 + col, v, q[g]);
+      };
+      if constexpr (NPRE > 0) {
+#pragma unroll
+        for (int g = 0; g < RG; ++g) visit(g);  // q[g] needs constant indices
+      } else {
 #pragma unroll 2
-      for (int g = 0; g < RG; ++g) visit(g);
+        for (int g = 0; g < RG; ++g) visit(g);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
   }
 }
 

@@ -1125,8 +1125,8 @@ using ThreeQuarterRows = Tiling<bf16_t, 3 * C::BM / 4, C::BN, C::BK, C::NW / 2, 
 template <typename T, class C>
 constexpr bool has_half_rows() { return sizeof(T) == 2 && C::BM == 256; }
 // The 3BM/4-row tiling's wave blocks are 96 rows tall; with eight waves and
-// two accumulator sets its epilogue staging would outgrow the LDS, and such
-// tails then run as full tiles.
+// two accumulator sets its epilogue stages them 32 rows at a time
+// (epi_rows), within the LDS.
 template <class C, int NACC>
 constexpr bool has_three_quarter_rows() {
   return epi_lds_floats<ThreeQuarterRows<C>, NACC>() * 4 <= kLdsBytes;
