@@ -25,7 +25,14 @@ namespace moe {
 
 // BM x BN output tile per workgroup of NW waves arranged WGM x WGN (wave w
 // owns block (w / WGN, w % WGN)), BK-deep k-tiles.
-template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2, int NST_ = 2, int NW_ = 4>
+//
+// XR > 0 ("tall" tile, direct-to-LDS loop only): the tile has XR = 64 more
+// rows below its BM rows, 2 x BN / 32 more 32 x 32 blocks shared out over the
+// four wave rows: wave (wm, wn) also owns extra row block wm & 1 (rows BM +
+// 32 (wm & 1) ..) at the XTN = WN / 64 column blocks of half wm >> 1 of its
+// own WN columns, whose B fragments it already reads for its main blocks.
+template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2, int NST_ = 2, int NW_ = 4,
+          int XR_ = 0>
 struct Tiling {
   static constexpr int BM = BM_, BN = BN_, BK = BK_;
   static constexpr int NST = NST_;        // LDS pipeline stages (direct-to-LDS loop)
@@ -36,11 +43,16 @@ struct Tiling {
   static constexpr int WGN = WGN_, WGM = NW_ / WGN_;  // wave grid
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // per-wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA blocks per wave
+  static constexpr int XR = XR_;                    // extra rows of a tall tile
+  static constexpr int XTN = XR > 0 ? WN / 64 : 1;  // extra column blocks per wave
+  static constexpr int AR = BM + XR;                // A-operand rows per k-tile
   static_assert(WGM * WGN == NW && (NW == 4 || NW == 8), "four or eight waves");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tiles of whole 32 x 32 blocks");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % (2 * V) == 0, "BK must cover whole MFMA k-steps");
   static_assert(NST >= 2 && NST <= 6, "2 to 6 pipeline stages");
+  static_assert(XR == 0 || (XR == 64 && WGM == 4 && WN % 64 == 0 && sizeof(T) == 2),
+                "tall tiles: 64 extra rows over a four-row wave grid, bf16");
 };
 
 // Source of one operand tile.  K-contiguous: element (r, k) at base + r*ld + k;
@@ -345,14 +357,22 @@ struct DmaStagerT {
 // runs in three phases without a data-dependent branch around the DMA:
 // k-tiles that refill a stage (kt + NST < nk), then the k-tiles whose DMA is
 // all in flight, then the last one.
+//
+// Tall tiles (C::XR > 0, K-contiguous A): the A tile holds C::AR rows and each
+// wave also multiplies its extra A fragment (row block wm & 1 of the XR extra
+// rows) with the B fragments of half wm >> 1 of its columns into xacc, which
+// are picked out of the registers it already holds (a wave-uniform select).
 template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
-MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
+MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
+                          f32x16 (&xacc)[NA * NB][C::XTN], const OpDesc<T> (&a)[NA],
                           const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2,
                           const OpDesc<T>* b2, int K2) {
-  constexpr int TILE_A = C::BM * C::BK, TILE_B = C::BN * C::BK;
+  constexpr int TILE_A = C::AR * C::BK, TILE_B = C::BN * C::BK;
   constexpr int STAGE = NA * TILE_A + NB * TILE_B;
   constexpr int NST = C::NST;
-  using SA = typename std::conditional<A_T, DmaStagerT<C, T, C::BM>, DmaStager<C, T, C::BM>>::type;
+  constexpr bool TALL = C::XR > 0;
+  static_assert(!TALL || !A_T, "tall tiles take a K-contiguous A operand");
+  using SA = typename std::conditional<A_T, DmaStagerT<C, T, C::AR>, DmaStager<C, T, C::AR>>::type;
   using SB = typename std::conditional<B_T, DmaStagerT<C, T, C::BN>, DmaStager<C, T, C::BN>>::type;
   // DMA instructions one wave issues per k-tile
   constexpr int IPT = NA * SA::PER + NB * SB::PER;
@@ -391,16 +411,21 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
   const int frag_kv = lane >> 5;
   constexpr int KSTEPS = C::BK / (2 * C::V);
   static_assert(KSTEPS % 2 == 0, "the next tile's first fragments go to register set 0");
-  u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN];
+  u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN], afx[2][NA];
+  // tall tiles: the wave's extra row block and column half (wave-uniform)
+  const int xrow = C::BM + 32 * (wm & 1) + frag_row;
+  const bool xhi = __builtin_amdgcn_readfirstlane(wm >> 1) != 0;
   auto read_frags = [&](const T* sA, const T* sB, int ks, int set) {
     const int kv = ks * 2 + frag_kv;
 #pragma unroll
-    for (int i = 0; i < NA; ++i)
+    for (int i = 0; i < NA; ++i) {
 #pragma unroll
       for (int tm = 0; tm < C::TM; ++tm) {
         if constexpr (A_T) af[set][i][tm] = SA::frag(sA + i * TILE_A, wm * C::WM + tm * 32, ks * 16);
         else af[set][i][tm] = SA::frag(sA + i * TILE_A, wm * C::WM + tm * 32 + frag_row, kv);
       }
+      if constexpr (TALL) afx[set][i] = SA::frag(sA + i * TILE_A, xrow, kv);
+    }
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
@@ -459,20 +484,28 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> 
 #pragma unroll
       for (int ia = 0; ia < NA; ++ia)
 #pragma unroll
-        for (int ib = 0; ib < NB; ++ib)
+        for (int ib = 0; ib < NB; ++ib) {
 #pragma unroll
           for (int tn = 0; tn < C::TN; ++tn)
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
               mfma_frag(acc[ia * NB + ib][tn][tm], bfr[cur][ib][tn], af[cur][ia][tm], T());
+          if constexpr (TALL) {
+#pragma unroll
+            for (int j = 0; j < C::XTN; ++j) {
+              const u32x4 bx = xhi ? bfr[cur][ib][C::XTN + j] : bfr[cur][ib][j];
+              mfma_frag(xacc[ia * NB + ib][j], bx, afx[cur][ia], T());
+            }
+          }
+        }
       if constexpr (phase == 0) {
         if (ks + 1 == KSTEPS) {
-          constexpr int NM = NA * NB * C::TN * C::TM;
+          constexpr int NM = NA * NB * (C::TN * C::TM + (TALL ? C::XTN : 0));
           // scheduling groups (masks: 0x100 LDS reads, 0x008 MFMA, 0x020
           // vector memory reads): the next tile's first fragment reads (two
           // per fragment of a transposed operand), then one DMA instruction
           // after each MFMA while they last
-          __builtin_amdgcn_sched_group_barrier(0x100, (NA * C::TM * (A_T ? 2 : 1)) + (NB * C::TN * (B_T ? 2 : 1)), 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, (NA * (C::TM + (TALL ? 1 : 0)) * (A_T ? 2 : 1)) + (NB * C::TN * (B_T ? 2 : 1)), 0);
 #pragma unroll
           for (int i = 0; i < NM; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -499,7 +532,7 @@ constexpr int stage_elems() { return (NA * C::BM + NB * C::BN) * C::LDK; }
 // unpadded; fp32 keeps the padded pitch of the register-staged loop.
 template <class C, int NA, int NB>
 constexpr int smem_elems() {
-  return C::V == 8 ? C::NST * (NA * C::BM + NB * C::BN) * C::BK : 2 * stage_elems<C, NA, NB>();
+  return C::V == 8 ? C::NST * (NA * C::AR + NB * C::BN) * C::BK : 2 * stage_elems<C, NA, NB>();
 }
 
 // acc[a * NB + b][tn][tm] += B_b-tile x A_a-tile over k in [0, K).
@@ -517,9 +550,11 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
                       const OpDesc<T>* b2 = nullptr, int K2 = 0) {
   // DMA for every bf16 operand layout; fp32 K-major operands keep the
   // register-staged transpose below (the transposing LDS read is 16-bit)
+  static_assert(C::XR == 0, "tall tiles run mainloop_x");
   if constexpr (sizeof(T) == 2 || (!A_T && !B_T)) {
     static_assert(C::NST * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
-    mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, a, b, K, smem, a2, b2, K2);
+    f32x16 unused[NA * NB][C::XTN];
+    mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, unused, a, b, K, smem, a2, b2, K2);
     return;
   }
   constexpr int STAGE = stage_elems<C, NA, NB>();
@@ -615,6 +650,19 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
   }
 }
 
+// mainloop for a row tile that may be tall (C::XR > 0, bf16): xacc holds the
+// wave's extra blocks (unused when C::XR == 0).
+template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
+MOE_DEV void mainloop_x(f32x16 (&acc)[NA * NB][C::TN][C::TM], f32x16 (&xacc)[NA * NB][C::XTN],
+                        const OpDesc<T> (&a)[NA], const OpDesc<T> (&b)[NB], int K, T* smem,
+                        const OpDesc<T>* a2 = nullptr, const OpDesc<T>* b2 = nullptr,
+                        int K2 = 0) {
+  if constexpr (C::XR > 0)
+    mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, xacc, a, b, K, smem, a2, b2, K2);
+  else
+    mainloop<C, T, A_T, B_T, NA, NB>(acc, a, b, K, smem, a2, b2, K2);
+}
+
 template <class C, int NACC>
 MOE_DEV void zero_acc(f32x16 (&acc)[NACC][C::TN][C::TM]) {
 #pragma unroll
@@ -625,6 +673,16 @@ MOE_DEV void zero_acc(f32x16 (&acc)[NACC][C::TN][C::TM]) {
       for (int tm = 0; tm < C::TM; ++tm)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[x][tn][tm][r] = 0.0f;
+}
+template <class C, int NACC>
+MOE_DEV void zero_acc(f32x16 (&acc)[NACC][C::TN][C::TM], f32x16 (&xacc)[NACC][C::XTN]) {
+  zero_acc<C, NACC>(acc);
+#pragma unroll
+  for (int x = 0; x < NACC; ++x)
+#pragma unroll
+    for (int j = 0; j < C::XTN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) xacc[x][j][r] = 0.0f;
 }
 
 // Calls f(m_local, n_local, v) for every 4-wide output fragment of the tile,
@@ -752,6 +810,67 @@ template <class C, int NACC, class F>
 MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, F&& f) {
   for_each_row8_pre<C, NACC, 0>(acc, lds, [](int, int, u32x4*) {},
                                 [&](int m, int n, auto& v, const u32x4*) { f(m, n, v); });
+}
+
+// for_each_row8_pre over a tile that may be tall: the main blocks, then the
+// wave's extra blocks (C::XR > 0: rows BM + 32 (wm & 1) .., columns of half
+// wm >> 1 of its WN), staged the same way, 32 rows at a time.
+template <class C, int NACC, int NPRE, class PRE, class F>
+MOE_DEV void for_each_row8_xpre(const f32x16 (&acc)[NACC][C::TN][C::TM],
+                                const f32x16 (&xacc)[NACC][C::XTN], float* lds, PRE&& pre,
+                                F&& f) {
+  for_each_row8_pre<C, NACC, NPRE>(acc, lds, pre, f);
+  if constexpr (C::XR > 0) {
+    constexpr int P = 36;
+    constexpr int NQ = NPRE > 0 ? NPRE : 1;
+    constexpr int SR = epi_rows<C, NACC>();
+    static_assert(SR >= 32, "one 32-row block per pass");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm = wave / C::WGN, wn = wave % C::WGN;
+    float* reg = lds + wave * NACC * SR * P;
+    const int r0 = C::BM + 32 * (wm & 1);
+    const int c0 = wn * C::WN + (wm >> 1) * (C::WN / 2);
+#pragma unroll
+    for (int j = 0; j < C::XTN; ++j) {
+      u32x4 q[2][NQ];
+      if constexpr (NPRE > 0) {
+#pragma unroll
+        for (int g = 0; g < 2; ++g) pre(r0 + g * 16 + (lane >> 2), c0 + j * 32 + (lane & 3) * 8, q[g]);
+      }
+#pragma unroll
+      for (int x = 0; x < NACC; ++x)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int row = lane & 31;
+          const int col = 8 * qq + 4 * (lane >> 5);
+          *reinterpret_cast<f32x4*>(reg + (x * SR + row) * P + col) =
+              f32x4{xacc[x][j][4 * qq], xacc[x][j][4 * qq + 1], xacc[x][j][4 * qq + 2],
+                    xacc[x][j][4 * qq + 3]};
+        }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int row = g * 16 + (lane >> 2);
+        const int col = (lane & 3) * 8;
+        float v[NACC][8];
+#pragma unroll
+        for (int x = 0; x < NACC; ++x) {
+          const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col);
+          const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col + 4);
+          v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
+          v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
+        }
+        f(r0 + row, c0 + j * 32 + col, v, q[g]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+}
+template <class C, int NACC, class F>
+MOE_DEV void for_each_row8_x(const f32x16 (&acc)[NACC][C::TN][C::TM],
+                             const f32x16 (&xacc)[NACC][C::XTN], float* lds, F&& f) {
+  for_each_row8_xpre<C, NACC, 0>(acc, xacc, lds, [](int, int, u32x4*) {},
+                                 [&](int m, int n, auto& v, const u32x4*) { f(m, n, v); });
 }
 
 // Row epilogue for bf16 outputs that need no element-wise work beyond a scale:

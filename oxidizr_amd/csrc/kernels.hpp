@@ -60,19 +60,22 @@ template <> struct Tilings<float> {
 // offsets == nullptr means one dense group of M rows.
 // A group of c rows has c / BM full row tiles and, when r = c % BM is not 0, a
 // last tile of r rows.  That tile counts among the "big" tiles when r > BM / 2
-// and is a "half" tile otherwise.  Tiles run group by group (a group's tiles
-// share its weight panels in L2), or, with half_last, every half tile after
-// every big tile: the half-height tiles then fill the last round of the launch
+// and is a "half" tile otherwise.  With tall > 0, a tail of 0 < r <= tall rows
+// behind at least one full tile has no tile of its own: the group's last full
+// tile covers BM + r rows.  Tiles run group by group (a group's tiles share
+// its weight panels in L2), or, with half_last, every half tile after every
+// big tile: the half-height tiles then fill the last round of the launch
 // instead of adding a round among the big tiles, at the cost of reading their
 // group's weights once more.
 struct RowGroups {
   const int* offsets;      // [G + 1] row offsets
-  const int* tile_prefix;  // [G + 1] prefix of the row tiles: ceil(c / BM)
+  const int* tile_prefix;  // [G + 1] prefix of the row tiles: ceil(c / BM) - merged
   const int* big_prefix;   // [G + 1] prefix of the big row tiles: c / BM + (r > BM / 2)
-  const int* half_prefix;  // [G + 1] prefix of the half row tiles: 0 < r <= BM / 2
+  const int* half_prefix;  // [G + 1] prefix of the half row tiles: 0 < r <= BM / 2, not merged
   int G;
   int M;                   // rows in all groups (the extent of row-major operands)
   int half_last;
+  int tall;                // tail rows the last full tile takes (0 or BM / 4)
 };
 
 // Tile coordinates are workgroup-uniform, but integer division by a runtime
@@ -163,7 +166,9 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
   const int rows = g.offsets[grp + 1] - g.offsets[grp];
   local = local < 0 ? (rows / BM) * BM : local * BM;  // -1: the group's half tile
   row0 = uni(g.offsets[grp] + local);
-  mv = uni(min(BM, rows - local));
+  // more than BM rows only for the last full tile with its merged tail
+  const int left = rows - local;
+  mv = uni(left > BM + g.tall ? BM : left);
   return mv > 0;
 }
 
@@ -300,7 +305,7 @@ __global__ __launch_bounds__(256) void k_router_logits(const T* __restrict__ x,
                                                        float* __restrict__ logits, int Tn, int H,
                                                        int E) {
   __shared__ __align__(16) T smem[kernel_smem_elems<C, T, 1, 1, 1>()];
-  RowGroups g{nullptr, nullptr, nullptr, nullptr, 1, Tn, 0};
+  RowGroups g{nullptr, nullptr, nullptr, nullptr, 1, Tn, 0, 0};
   int grp, row0, mv, n0;
   if (!resolve_rows(g, E, C::BM, C::BN, grp, row0, mv, n0)) return;
   OpDesc<T> a[1] = {{x + (int64_t)row0 * H, H, mv, H}};
@@ -724,6 +729,10 @@ __global__ __launch_bounds__(256) void k_hist(const int* __restrict__ idx, int T
 constexpr int kTilePrefixes = 3;
 constexpr int kNumTileBM = 2;
 __constant__ int kTileBM[kNumTileBM] = {128, 256};
+// Tail rows a group's last full row tile takes (RowGroups::tall) for row
+// tiles of height bm: the bf16 256-row tilings run it as a tall tile; fp32's
+// 128-row tiles take none.
+constexpr int tall_rows_for(int bm) { return bm == 256 ? bm / 4 : 0; }
 
 // Inclusive prefix sums across the 64 lanes of a wave of N values at once:
 // each step issues the N shuffles before adding, so the N scans wait for one
@@ -760,9 +769,12 @@ MOE_DEV void scan_counts(const int* cnt, int E, int* __restrict__ offsets,
     v[j] = c;
     if (j > 0) {
       const int bm = kTileBM[(j - 1) / kTilePrefixes], r = c % bm, kind = (j - 1) % kTilePrefixes;
-      v[j] = kind == 0 ? (c + bm - 1) / bm
+      // a short tail behind a full tile joins that tile (tall tile)
+      const int merged = c > bm && r > 0 && r <= tall_rows_for(bm) ? 1 : 0;
+      const int tail = r > 0 && !merged ? 1 : 0;
+      v[j] = kind == 0 ? c / bm + tail
            : kind == 1 ? c / bm + (r > bm / 2 ? 1 : 0)
-                       : (r > 0 && r <= bm / 2 ? 1 : 0);
+                       : (tail && r <= bm / 2 ? 1 : 0);
     }
     incl[j] = v[j];
   }
@@ -1124,6 +1136,13 @@ template <class C>
 using ThreeQuarterRows = Tiling<bf16_t, 3 * C::BM / 4, C::BN, C::BK, C::NW / 2, C::NST, C::NW>;
 template <typename T, class C>
 constexpr bool has_half_rows() { return sizeof(T) == 2 && C::BM == 256; }
+// A group's last full row tile also takes a tail of at most BM / 4 rows
+// (TallRows: BM + BM / 4 rows, the tail's blocks shared out over the waves,
+// which reuse their B fragments), instead of a BM / 4-row tile that streams
+// the group's whole weight panel again.  Every bf16 256-row tiling of the
+// row-grouped GEMMs has it (their tile prefixes count tiles that way).
+template <class C>
+using TallRows = Tiling<bf16_t, C::BM, C::BN, C::BK, C::WGN, C::NST, C::NW, C::BM / 4>;
 // The 3BM/4-row tiling's wave blocks are 96 rows tall; with eight waves and
 // two accumulator sets its epilogue stages them 32 rows at a time
 // (epi_rows), within the LDS.
@@ -1139,17 +1158,23 @@ constexpr int rowgroup_smem_elems() {
     constexpr int c = kernel_smem_elems<HalfRows<C>, T, NA, NB, NACC>();
     constexpr int d = has_three_quarter_rows<C, NACC>()
                           ? kernel_smem_elems<ThreeQuarterRows<C>, T, NA, NB, NACC>() : 0;
-    constexpr int ab = a > b ? a : b, cd = c > d ? c : d;
-    return ab > cd ? ab : cd;
+    constexpr int e = kernel_smem_elems<TallRows<C>, T, NA, NB, NACC>();
+    constexpr int ab = a > b ? a : b, cd = c > d ? c : d, abcd = ab > cd ? ab : cd;
+    return abcd > e ? abcd : e;
   } else {
     return a;
   }
 }
 // Runs body(tiling) for a resolved row tile with mv valid rows: the shortest
-// row tiling that covers them (NACC: the kernel's accumulator sets).
+// row tiling that covers them (NACC: the kernel's accumulator sets); more than
+// BM rows (a group's last full tile with its short tail) run as the tall tile.
 template <typename T, class C, int NACC, class F>
 MOE_DEV void with_tile_rows(int mv, F&& body) {
   if constexpr (has_half_rows<T, C>()) {
+    if (mv > C::BM) {
+      body(TallRows<C>{});
+      return;
+    }
     if (mv <= C::BM / 4) {
       body(QuarterRows<C>{});
       return;
@@ -1186,12 +1211,17 @@ constexpr int rowcol_smem_elems() {
     return a;
   }
 }
-// body(tiling): a BM/4- or BM/2-row tiling when that covers the mv valid rows,
-// else the half-width tiling when at most BN / 2 of the nv remaining columns
-// are valid, else the 3BM/4-row tiling when that covers the rows, else C.
+// body(tiling): the tall tiling for more than BM rows, a BM/4- or BM/2-row
+// tiling when that covers the mv valid rows, else the half-width tiling when
+// at most BN / 2 of the nv remaining columns are valid, else the 3BM/4-row
+// tiling when that covers the rows, else C.
 template <typename T, class C, class F>
 MOE_DEV void with_tile_shape(int mv, int nv, F&& body) {
   if constexpr (has_half_rows<T, C>()) {
+    if (mv > C::BM) {  // full width even when at most BN / 2 columns are valid
+      body(TallRows<C>{});
+      return;
+    }
     if (mv <= C::BM / 4) {
       body(QuarterRows<C>{});
       return;
@@ -1233,11 +1263,11 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_fwd(const T* __restrict__
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{X + (int64_t)row0 * H, H, mv, H}};
     OpDesc<T> b[2] = {{wg + (int64_t)n0 * H, H, N - n0, H}, {wu + (int64_t)n0 * H, H, N - n0, H}};
-    f32x16 acc[2][CT::TN][CT::TM];
-    zero_acc<CT, 2>(acc);
-    mainloop<CT, T, false, false, 1, 2>(acc, a, b, H, smem);
+    f32x16 acc[2][CT::TN][CT::TM], xacc[2][CT::XTN];
+    zero_acc<CT, 2>(acc, xacc);
+    mainloop_x<CT, T, false, false, 1, 2>(acc, xacc, a, b, H, smem);
     static_assert(epi_lds_floats<CT, 2>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8<CT, 2>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+    for_each_row8_x<CT, 2>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
       if (m >= mv || n0 + n >= N) return;
       float act[8];
 #pragma unroll
@@ -1265,11 +1295,11 @@ __global__ __launch_bounds__(C::THREADS) void k_down_fwd(const T* __restrict__ A
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{A + (int64_t)row0 * I, I, mv, I}};
     OpDesc<T> b[1] = {{wd + (int64_t)n0 * I, I, H - n0, I}};
-    f32x16 acc[1][CT::TN][CT::TM];
-    zero_acc<CT, 1>(acc);
-    mainloop<CT, T, false, false, 1, 1>(acc, a, b, I, smem);
+    f32x16 acc[1][CT::TN][CT::TM], xacc[1][CT::XTN];
+    zero_acc<CT, 1>(acc, xacc);
+    mainloop_x<CT, T, false, false, 1, 1>(acc, xacc, a, b, I, smem);
     static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8<CT, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+    for_each_row8_x<CT, 1>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
       if (m >= mv || n0 + n >= H) return;
       store8(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
     });
@@ -1413,11 +1443,11 @@ __global__ __launch_bounds__(C::THREADS) void k_down_dgrad(const T* __restrict__
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{dY + (int64_t)row0 * H, H, mv, H}};
     OpDesc<T> b[1] = {{wd + n0, N, N - n0, H}};
-    f32x16 acc[1][CT::TN][CT::TM];
-    zero_acc<CT, 1>(acc);
-    mainloop<CT, T, false, true, 1, 1>(acc, a, b, H, smem);
+    f32x16 acc[1][CT::TN][CT::TM], xacc[1][CT::XTN];
+    zero_acc<CT, 1>(acc, xacc);
+    mainloop_x<CT, T, false, true, 1, 1>(acc, xacc, a, b, H, smem);
     static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8_pre<CT, 1, 2 * NV>(acc, reinterpret_cast<float*>(smem), pre,
+    for_each_row8_xpre<CT, 1, 2 * NV>(acc, xacc, reinterpret_cast<float*>(smem), pre,
                                      [&](int m, int n, auto& v, const u32x4 (&q)[2 * NV]) {
       if (m >= mv || n0 + n >= N) return;
       const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
@@ -1454,16 +1484,16 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_dgrad(const T* __restrict
   const T* wu = pick(wu_tab, wu_one, grp);
   with_tile_rows<T, C, 1>(mv, [&](auto ct) {
     using CT = decltype(ct);
-    f32x16 acc[1][CT::TN][CT::TM];
-    zero_acc<CT, 1>(acc);
+    f32x16 acc[1][CT::TN][CT::TM], xacc[1][CT::XTN];
+    zero_acc<CT, 1>(acc, xacc);
     // one pipelined loop over K = 2I: the dG / Wg segment, then dU / Wu
     OpDesc<T> a[1] = {{dG + (int64_t)row0 * I, I, mv, I}};
     OpDesc<T> b[1] = {{wg + n0, H, H - n0, I}};
     OpDesc<T> a2[1] = {{dU + (int64_t)row0 * I, I, mv, I}};
     OpDesc<T> b2[1] = {{wu + n0, H, H - n0, I}};
-    mainloop<CT, T, false, true, 1, 1>(acc, a, b, I, smem, a2, b2, I);
+    mainloop_x<CT, T, false, true, 1, 1>(acc, xacc, a, b, I, smem, a2, b2, I);
     static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8<CT, 1>(acc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+    for_each_row8_x<CT, 1>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
       if (m >= mv || n0 + n >= H) return;
       store8(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
     });

@@ -729,7 +729,7 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
                          (const bf16_t*)sA, nullptr, 1, 0, nullptr, 1, T, nullptr, (const bf16_t*)w->shared_down,
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else {
-    const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
+    const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0, 0};
     hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
                        dim3(CG::THREADS), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
                        (const D*)w->shared_up, H, S, sG, sU, sA);
@@ -753,7 +753,11 @@ void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t 
   const int* tp = tprefix_all + kTilePrefixes * tile_slot(C::BM) * (E + 1);
   const int mt = ceil_div(TK, C::BM) + E;
   const int half_last = has_half_rows<D, C>() && TK >= 2 * (int64_t)C::BM * E;
-  f(C{}, RowGroups{offsets, tp, tp + (E + 1), tp + 2 * (E + 1), E, (int)TK, half_last},
+  // the prefixes (k_scan) merge short tails into tall tiles exactly where the
+  // kernels' row tilings have them
+  static_assert(tall_rows_for(C::BM) == (has_half_rows<D, C>() ? C::BM / 4 : 0), "tall tiles");
+  f(C{}, RowGroups{offsets, tp, tp + (E + 1), tp + 2 * (E + 1), E, (int)TK, half_last,
+                   tall_rows_for(C::BM)},
     [mt](int N) { return 8 * ceil_div(mt * ceil_div(N, C::BN), 8); });
 }
 
@@ -1054,7 +1058,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     D* sdU = (D*)(ws + W.sdU);
     dxs = (D*)(ws + W.dxs);
     const float sc = c.shared_expert_scale;
-    const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0};
+    const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0, 0};
     hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(CB::THREADS), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
                        sdG, sdU);
     hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(CB::THREADS), 0, ss, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,

@@ -192,6 +192,41 @@ def test_bf16_forward_backward_parity(spec):
     _check(case, g, o, 1e-2)
 
 
+TALL_CASES = [
+    # E = 2, k = 2: every expert receives all T tokens, so the counts are T.
+    # 300 and 320 rows: one 256-row tile that also takes the 44 / 64-row tail
+    # (tall tile); 321: the tail (65 rows) keeps its own tile.
+    dict(T=300, H=128, E=2, k=2, I=96, S=0),
+    dict(T=320, H=320, E=2, k=2, I=296, S=32),
+    dict(T=321, H=128, E=2, k=2, I=64, S=0),
+    # 560 rows = 2 x 256 + 48 with >= 512 rows per expert (tails run last):
+    # the second full tile is tall; I = 296 leaves a last column tile of 40
+    # (the input gradient of the down projection runs it at full width)
+    dict(T=560, H=136, E=2, k=2, I=296, S=0),
+    # random counts around 300 rows (some merged tails, some not), router bias
+    dict(T=1200, H=128, E=8, k=2, I=88, S=16, bias=True),
+]
+
+
+@pytest.mark.parametrize("spec", TALL_CASES)
+def test_bf16_tall_tile_parity(spec):
+    """Row groups whose last full 256-row tile also takes a tail of at most 64
+    rows (one 320-row tile instead of a full and a quarter tile)."""
+    spec = dict(spec)
+    bias = zipf_bias(spec["E"], beta=0.3) if spec.pop("bias", False) else None
+    case = Case(**spec, dtype="bf16", w_std=0.05, bias=bias)
+    g = gpu_run(case, d_aux=0.01, d_z=0.001)
+    o = oracle_run(case, g["logits"], d_aux=0.01, d_z=0.001)
+    _routing_equal(g, o)
+    counts = np.asarray(g["counts"])
+    merged = (counts > 256) & (counts % 256 > 0) & (counts % 256 <= 64)
+    if spec["T"] == 321:
+        assert not merged.any(), counts
+    else:
+        assert merged.any(), counts
+    _check(case, g, o, 1e-2)
+
+
 SKINNY_CASES = [
     # T <= 64: the forward streams expert weights (skinny kernels); backward
     # runs the tiled kernels on the skinny forward's saved activations
