@@ -164,6 +164,19 @@ MOE_DEV bool resolve_rows(const RowGroups& g, int N, int BM, int BN, int& grp, i
   }
   n0 = nt * BN;
   const int rows = g.offsets[grp + 1] - g.offsets[grp];
+  if (g.tall > 0 && !g.half_last) {
+    // a tail of tall < r <= BM / 2 rows and the full tile before it run as two
+    // 3BM/4-row tiles (3BM/4 and BM/4 + r rows): tiles of equal speed stay
+    // together on their XCD and read the group's weight panels from its L2
+    // once (config 5: step -0.25 %)
+    const int nfull = rows / BM, r = rows - nfull * BM;
+    if (nfull >= 1 && r > g.tall && r <= BM / 2 && local >= nfull - 1) {
+      const int off = (nfull - 1) * BM + (local == nfull ? 3 * BM / 4 : 0);
+      row0 = uni(g.offsets[grp] + off);
+      mv = uni(local == nfull ? rows - off : 3 * BM / 4);
+      return true;
+    }
+  }
   local = local < 0 ? (rows / BM) * BM : local * BM;  // -1: the group's half tile
   row0 = uni(g.offsets[grp] + local);
   // more than BM rows only for the last full tile with its merged tail
