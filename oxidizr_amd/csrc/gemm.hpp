@@ -742,7 +742,8 @@ constexpr int kernel_smem_elems() {
 // With NPRE > 0, pre(m_local, n_local, q) is called for every row of a block
 // before any row of it is visited: it issues the NPRE 16-byte loads the visit
 // needs into q, so a block's loads are all in flight together instead of
-// being waited for row group by row group.
+// being waited for row group by row group, and the next block's loads are
+// issued before this block's rows are visited.
 template <class C, int NACC, int NPRE, class PRE, class F>
 MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, PRE&& pre,
                                F&& f) {
@@ -752,57 +753,63 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
   constexpr int SR = epi_rows<C, NACC>();  // rows staged per pass
   constexpr int NSP = C::WM / SR;          // passes per 32-column block
   constexpr int RG = SR / 16;              // row groups of a pass
+  constexpr int NPASS = C::TN * NSP;       // passes of the wave's block
   static_assert(C::WM % SR == 0 && SR % 32 == 0, "whole MFMA blocks per pass");
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
   float* reg = lds + wave * NACC * SR * P;
+  // the loads of pass b + 1 are issued before the rows of pass b are visited
+  // (two register sets), so their latency overlaps one pass of work
+  u32x4 q[2][RG][NQ];
+  auto prefetch = [&](int b, int set) {
+    const int r0 = wm * C::WM + (b % NSP) * SR;
 #pragma unroll
-  for (int tn = 0; tn < C::TN; ++tn) {  // unrolled: acc is indexed by constants only
+    for (int g = 0; g < RG; ++g)
+      pre(r0 + g * 16 + (lane >> 2), wn * C::WN + (b / NSP) * 32 + (lane & 3) * 8, q[set][g]);
+  };
+  if constexpr (NPRE > 0) prefetch(0, 0);
 #pragma unroll
-    for (int sp = 0; sp < NSP; ++sp) {
-      const int r0 = wm * C::WM + sp * SR;  // first row of this pass
-      u32x4 q[RG][NQ];
-      if constexpr (NPRE > 0) {
-#pragma unroll
-        for (int g = 0; g < RG; ++g)
-          pre(r0 + g * 16 + (lane >> 2), wn * C::WN + tn * 32 + (lane & 3) * 8, q[g]);
-      }
-#pragma unroll
-      for (int x = 0; x < NACC; ++x)
-#pragma unroll
-        for (int tl = 0; tl < SR / 32; ++tl)
-#pragma unroll
-          for (int qq = 0; qq < 4; ++qq) {
-            const int tm = sp * (SR / 32) + tl;
-            const int row = tl * 32 + (lane & 31);
-            const int col = 8 * qq + 4 * (lane >> 5);
-            *reinterpret_cast<f32x4*>(reg + (x * SR + row) * P + col) =
-                f32x4{acc[x][tn][tm][4 * qq], acc[x][tn][tm][4 * qq + 1],
-                      acc[x][tn][tm][4 * qq + 2], acc[x][tn][tm][4 * qq + 3]};
-          }
-      __builtin_amdgcn_sched_barrier(0);
-      auto visit = [&](int g) {
-        const int row = g * 16 + (lane >> 2);
-        const int col = (lane & 3) * 8;
-        float v[NACC][8];
-#pragma unroll
-        for (int x = 0; x < NACC; ++x) {
-          const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col);
-          const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col + 4);
-          v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
-          v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
-        }
-        f(r0 + row, wn * C::WN + tn * 32 + col, v, q[g]);
-      };
-      if constexpr (NPRE > 0) {
-#pragma unroll
-        for (int g = 0; g < RG; ++g) visit(g);  // q[g] needs constant indices
-      } else {
-#pragma unroll 2
-        for (int g = 0; g < RG; ++g) visit(g);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+  for (int b = 0; b < NPASS; ++b) {  // unrolled: acc is indexed by constants only
+    const int tn = b / NSP, sp = b % NSP, set = b & 1;
+    const int r0 = wm * C::WM + sp * SR;  // first row of this pass
+    if constexpr (NPRE > 0) {
+      if (b + 1 < NPASS) prefetch(b + 1, set ^ 1);
     }
+#pragma unroll
+    for (int x = 0; x < NACC; ++x)
+#pragma unroll
+      for (int tl = 0; tl < SR / 32; ++tl)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) {
+          const int tm = sp * (SR / 32) + tl;
+          const int row = tl * 32 + (lane & 31);
+          const int col = 8 * qq + 4 * (lane >> 5);
+          *reinterpret_cast<f32x4*>(reg + (x * SR + row) * P + col) =
+              f32x4{acc[x][tn][tm][4 * qq], acc[x][tn][tm][4 * qq + 1],
+                    acc[x][tn][tm][4 * qq + 2], acc[x][tn][tm][4 * qq + 3]};
+        }
+    __builtin_amdgcn_sched_barrier(0);
+    auto visit = [&](int g) {
+      const int row = g * 16 + (lane >> 2);
+      const int col = (lane & 3) * 8;
+      float v[NACC][8];
+#pragma unroll
+      for (int x = 0; x < NACC; ++x) {
+        const f32x4 lo = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col);
+        const f32x4 hi = *reinterpret_cast<const f32x4*>(reg + (x * SR + row) * P + col + 4);
+        v[x][0] = lo[0]; v[x][1] = lo[1]; v[x][2] = lo[2]; v[x][3] = lo[3];
+        v[x][4] = hi[0]; v[x][5] = hi[1]; v[x][6] = hi[2]; v[x][7] = hi[3];
+      }
+      f(r0 + row, wn * C::WN + tn * 32 + col, v, q[set][g]);
+    };
+    if constexpr (NPRE > 0) {
+#pragma unroll
+      for (int g = 0; g < RG; ++g) visit(g);  // q[set][g] needs constant indices
+    } else {
+#pragma unroll 2
+      for (int g = 0; g < RG; ++g) visit(g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
