@@ -461,15 +461,27 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
   // k-step refills the stage of kt with k-tile kt + NST; phase 1: every
   // k-tile is issued, the last k-step only moves on to kt + 1; phase 2: the
   // last k-tile.
+  // Weight gradients (both operands K-major; K = a group's tokens, ragged):
+  // the last k-tile runs only the k-steps that reach a valid k.  The others
+  // would multiply the zeros the buffer loads return past K, and nothing
+  // overlaps the last k-tile's MFMAs.  (The other GEMMs keep the full k-tile:
+  // their K is a model dimension, and the branch costs their registers.)
+  constexpr bool SKIPK = A_T && B_T;
+  const int klast = K2 > 0 ? K2 - (nk - nk1 - 1) * C::BK : K - (nk1 - 1) * C::BK;
+  const int kslast = SKIPK ? __builtin_amdgcn_readfirstlane((klast + 2 * C::V - 1) / (2 * C::V))
+                           : KSTEPS;
   auto body = [&](int kt, auto phase_c) {
     constexpr int phase = decltype(phase_c)::value;
     const T* sA = smem + stage_of(kt) * STAGE;
     const T* sB = sA + NA * TILE_A;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
+      if constexpr (phase == 2 && SKIPK) {
+        if (ks >= kslast) break;
+      }
       const int cur = ks & 1;
       if (ks + 1 < KSTEPS) {
-        read_frags(sA, sB, ks + 1, cur ^ 1);
+        if (phase < 2 || !SKIPK || ks + 1 < kslast) read_frags(sA, sB, ks + 1, cur ^ 1);
       } else if constexpr (phase < 2) {
         if constexpr (phase == 0) {
           asm volatile("s_waitcnt vmcnt(%0)" :: "n"((NST - 2) * IPT) : "memory");
