@@ -362,6 +362,14 @@ struct DmaStagerT {
 // wave also multiplies its extra A fragment (row block wm & 1 of the XR extra
 // rows) with the B fragments of half wm >> 1 of its columns into xacc, which
 // are picked out of the registers it already holds (a wave-uniform select).
+// Workgroup barrier of the direct-to-LDS pipeline: this wave's LDS reads are
+// done (s_waitcnt lgkmcnt(0)) and every wave has passed its own explicit
+// vmcnt wait for the k-tile it needs next.  __syncthreads() compiles to
+// s_waitcnt vmcnt(0) lgkmcnt(0) before s_barrier: it would also wait for the
+// DMA of every later k-tile already in flight, which drains a pipeline of more
+// than two stages at each k-tile.
+MOE_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
 MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
                           f32x16 (&xacc)[NA * NB][C::XTN], const OpDesc<T> (&a)[NA],
@@ -450,7 +458,7 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
   };
   static_assert(NST <= 5, "wait_tile covers up to three later tiles");
   wait_tile(0, pro - 1);
-  __syncthreads();
+  lds_barrier();
   int issued = pro - 1;
   if (NST - 1 < nk) {
     issue(NST - 1);
@@ -488,7 +496,7 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
         } else {
           wait_tile(kt + 1, issued);
         }
-        __syncthreads();
+        lds_barrier();
         const T* nA = smem + stage_of(kt + 1) * STAGE;
         read_frags(nA, nA + NA * TILE_A, 0, cur ^ 1);
         if constexpr (phase == 0) issue(kt + NST);
