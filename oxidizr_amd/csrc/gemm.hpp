@@ -26,11 +26,14 @@ namespace moe {
 // BM x BN output tile per workgroup of NW waves arranged WGM x WGN (wave w
 // owns block (w / WGN, w % WGN)), BK-deep k-tiles.
 //
-// XR > 0 ("tall" tile, direct-to-LDS loop only): the tile has XR = 64 more
-// rows below its BM rows, 2 x BN / 32 more 32 x 32 blocks shared out over the
-// four wave rows: wave (wm, wn) also owns extra row block wm & 1 (rows BM +
-// 32 (wm & 1) ..) at the XTN = WN / 64 column blocks of half wm >> 1 of its
-// own WN columns, whose B fragments it already reads for its main blocks.
+// XR > 0 ("tall" tile, direct-to-LDS loop only): the tile has XR more rows
+// below its BM rows, shared out over the four wave rows.  XR = 64: wave
+// (wm, wn) also owns extra row block wm & 1 (rows BM + 32 (wm & 1) ..) at the
+// XTN = WN / 64 column blocks of half wm >> 1 of its own WN columns.  XR = 128:
+// wave (wm, wn) also owns extra row block wm (rows BM + 32 wm ..) at all TN
+// column blocks of its WN columns.  Either way the extra blocks use B
+// fragments the wave already reads for its main blocks.  XR = 128 keeps one
+// register set of fragments (FB1) to fit its 192 accumulators.
 template <typename T, int BM_, int BN_, int BK_, int WGN_ = 2, int NST_ = 2, int NW_ = 4,
           int XR_ = 0>
 struct Tiling {
@@ -44,15 +47,16 @@ struct Tiling {
   static constexpr int WM = BM / WGM, WN = BN / WGN;  // per-wave tile
   static constexpr int TM = WM / 32, TN = WN / 32;  // 32x32 MFMA blocks per wave
   static constexpr int XR = XR_;                    // extra rows of a tall tile
-  static constexpr int XTN = XR > 0 ? WN / 64 : 1;  // extra column blocks per wave
+  static constexpr int XTN = XR == 128 ? TN : XR > 0 ? WN / 64 : 1;  // extra column blocks per wave
   static constexpr int AR = BM + XR;                // A-operand rows per k-tile
+  static constexpr bool FB1 = XR == 128;            // one register set of fragments
   static_assert(WGM * WGN == NW && (NW == 4 || NW == 8), "four or eight waves");
   static_assert(WM % 32 == 0 && WN % 32 == 0, "wave tiles of whole 32 x 32 blocks");
   static_assert(BM % 64 == 0 && BN % 64 == 0, "tile must be a multiple of 64");
   static_assert(BK % (2 * V) == 0, "BK must cover whole MFMA k-steps");
   static_assert(NST >= 2 && NST <= 6, "2 to 6 pipeline stages");
-  static_assert(XR == 0 || (XR == 64 && WGM == 4 && WN % 64 == 0 && sizeof(T) == 2),
-                "tall tiles: 64 extra rows over a four-row wave grid, bf16");
+  static_assert(XR == 0 || (((XR == 64 && WN % 64 == 0) || XR == 128) && WGM == 4 && sizeof(T) == 2),
+                "tall tiles: 64 or 128 extra rows over a four-row wave grid, bf16");
 };
 
 // Source of one operand tile.  K-contiguous: element (r, k) at base + r*ld + k;
@@ -419,9 +423,10 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
   const int frag_kv = lane >> 5;
   constexpr int KSTEPS = C::BK / (2 * C::V);
   static_assert(KSTEPS % 2 == 0, "the next tile's first fragments go to register set 0");
-  u32x4 af[2][NA][C::TM], bfr[2][NB][C::TN], afx[2][NA];
+  constexpr int NSET = C::FB1 ? 1 : 2;
+  u32x4 af[NSET][NA][C::TM], bfr[NSET][NB][C::TN], afx[NSET][NA];
   // tall tiles: the wave's extra row block and column half (wave-uniform)
-  const int xrow = C::BM + 32 * (wm & 1) + frag_row;
+  const int xrow = C::BM + 32 * (C::XR == 128 ? wm : (wm & 1)) + frag_row;
   const bool xhi = __builtin_amdgcn_readfirstlane(wm >> 1) != 0;
   auto read_frags = [&](const T* sA, const T* sB, int ks, int set) {
     const int kv = ks * 2 + frag_kv;
@@ -464,7 +469,7 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
     issue(NST - 1);
     issued = NST - 1;
   }
-  read_frags(smem, smem + NA * TILE_A, 0, 0);
+  if constexpr (!C::FB1) read_frags(smem, smem + NA * TILE_A, 0, 0);
   // One k-tile.  Phase 0: k-tiles up to kt + NST - 1 are issued and the last
   // k-step refills the stage of kt with k-tile kt + NST; phase 1: every
   // k-tile is issued, the last k-step only moves on to kt + 1; phase 2: the
@@ -487,8 +492,23 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
       if constexpr (phase == 2 && SKIPK) {
         if (ks >= kslast) break;
       }
-      const int cur = ks & 1;
-      if (ks + 1 < KSTEPS) {
+      const int cur = C::FB1 ? 0 : ks & 1;
+      if constexpr (C::FB1) {
+        // one register set: this k-step's fragments, then (last k-step) the
+        // barrier for the next k-tile and the refill of this stage
+        read_frags(sA, sB, ks, 0);
+        if constexpr (phase < 2) {
+          if (ks + 1 == KSTEPS) {
+            if constexpr (phase == 0) {
+              asm volatile("s_waitcnt vmcnt(%0)" :: "n"((NST - 2) * IPT) : "memory");
+            } else {
+              wait_tile(kt + 1, issued);
+            }
+            lds_barrier();
+            if constexpr (phase == 0) issue(kt + NST);
+          }
+        }
+      } else if (ks + 1 < KSTEPS) {
         if (phase < 2 || !SKIPK || ks + 1 < kslast) read_frags(sA, sB, ks + 1, cur ^ 1);
       } else if constexpr (phase < 2) {
         if constexpr (phase == 0) {
@@ -510,7 +530,11 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
 #pragma unroll
             for (int tm = 0; tm < C::TM; ++tm)
               mfma_frag(acc[ia * NB + ib][tn][tm], bfr[cur][ib][tn], af[cur][ia][tm], T());
-          if constexpr (TALL) {
+          if constexpr (C::XR == 128) {
+#pragma unroll
+            for (int j = 0; j < C::XTN; ++j)
+              mfma_frag(xacc[ia * NB + ib][j], bfr[cur][ib][j], afx[cur][ia], T());
+          } else if constexpr (TALL) {
 #pragma unroll
             for (int j = 0; j < C::XTN; ++j) {
               const u32x4 bx = xhi ? bfr[cur][ib][C::XTN + j] : bfr[cur][ib][j];
@@ -525,7 +549,8 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
           // vector memory reads): the next tile's first fragment reads (two
           // per fragment of a transposed operand), then one DMA instruction
           // after each MFMA while they last
-          __builtin_amdgcn_sched_group_barrier(0x100, (NA * (C::TM + (TALL ? 1 : 0)) * (A_T ? 2 : 1)) + (NB * C::TN * (B_T ? 2 : 1)), 0);
+          if constexpr (!C::FB1)
+            __builtin_amdgcn_sched_group_barrier(0x100, (NA * (C::TM + (TALL ? 1 : 0)) * (A_T ? 2 : 1)) + (NB * C::TN * (B_T ? 2 : 1)), 0);
 #pragma unroll
           for (int i = 0; i < NM; ++i) {
             __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -779,21 +804,27 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
   const int wm = wave / C::WGN, wn = wave % C::WGN;
   float* reg = lds + wave * NACC * SR * P;
   // the loads of pass b + 1 are issued before the rows of pass b are visited
-  // (two register sets), so their latency overlaps one pass of work
-  u32x4 q[2][RG][NQ];
+  // (two register sets), so their latency overlaps one pass of work; the
+  // 384-row tiles, whose extra accumulators are live here, keep one set
+  constexpr int QS = C::XR == 128 ? 1 : 2;
+  u32x4 q[QS][RG][NQ];
   auto prefetch = [&](int b, int set) {
     const int r0 = wm * C::WM + (b % NSP) * SR;
 #pragma unroll
     for (int g = 0; g < RG; ++g)
       pre(r0 + g * 16 + (lane >> 2), wn * C::WN + (b / NSP) * 32 + (lane & 3) * 8, q[set][g]);
   };
-  if constexpr (NPRE > 0) prefetch(0, 0);
+  if constexpr (NPRE > 0 && QS == 2) prefetch(0, 0);
 #pragma unroll
   for (int b = 0; b < NPASS; ++b) {  // unrolled: acc is indexed by constants only
-    const int tn = b / NSP, sp = b % NSP, set = b & 1;
+    const int tn = b / NSP, sp = b % NSP, set = QS == 2 ? b & 1 : 0;
     const int r0 = wm * C::WM + sp * SR;  // first row of this pass
     if constexpr (NPRE > 0) {
-      if (b + 1 < NPASS) prefetch(b + 1, set ^ 1);
+      if constexpr (QS == 2) {
+        if (b + 1 < NPASS) prefetch(b + 1, set ^ 1);
+      } else {
+        prefetch(b, 0);
+      }
     }
 #pragma unroll
     for (int x = 0; x < NACC; ++x)
@@ -855,8 +886,8 @@ MOE_DEV void for_each_row8_xpre(const f32x16 (&acc)[NACC][C::TN][C::TM],
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm = wave / C::WGN, wn = wave % C::WGN;
     float* reg = lds + wave * NACC * SR * P;
-    const int r0 = C::BM + 32 * (wm & 1);
-    const int c0 = wn * C::WN + (wm >> 1) * (C::WN / 2);
+    const int r0 = C::BM + 32 * (C::XR == 128 ? wm : (wm & 1));
+    const int c0 = wn * C::WN + (C::XR == 128 ? 0 : (wm >> 1) * (C::WN / 2));
 #pragma unroll
     for (int j = 0; j < C::XTN; ++j) {
       u32x4 q[2][NQ];

@@ -740,8 +740,8 @@ __global__ __launch_bounds__(256) void k_hist(const int* __restrict__ idx, int T
 // row-tile heights in kTileBM: per height, the prefixes of all, big and half
 // row tiles (RowGroups), each [E + 1].
 constexpr int kTilePrefixes = 3;
-constexpr int kNumTileBM = 2;
-__constant__ int kTileBM[kNumTileBM] = {128, 256};
+constexpr int kNumTileBM = 3;
+__constant__ int kTileBM[kNumTileBM] = {128, 256, 384};
 // Tail rows a group's last full row tile takes (RowGroups::tall) for row
 // tiles of height bm: the bf16 256-row tilings run it as a tall tile; fp32's
 // 128-row tiles take none.
@@ -1156,6 +1156,15 @@ constexpr bool has_half_rows() { return sizeof(T) == 2 && C::BM == 256; }
 // row-grouped GEMMs has it (their tile prefixes count tiles that way).
 template <class C>
 using TallRows = Tiling<bf16_t, C::BM, C::BN, C::BK, C::WGN, C::NST, C::NW, C::BM / 4>;
+// 384-row tiles for launches whose groups average at least three 256-row
+// tiles: the BM rows of C and 128 more, one 32-row block per wave row at all
+// of its columns (one fragment register set, 250-256 VGPRs).  A k-tile then
+// brings 25 % more operand rows for 50 % more MFMA work.  Row tiles of at most
+// BM + BM / 4 rows run as C's tilings (RowBase).
+template <class C>
+using Rows384 = Tiling<bf16_t, C::BM, C::BN, C::BK, C::WGN, C::NST, C::NW, C::BM / 2>;
+template <class C>
+using RowBase = Tiling<bf16_t, C::BM, C::BN, C::BK, C::WGN, C::NST, C::NW>;
 // The 3BM/4-row tiling's wave blocks are 96 rows tall; with eight waves and
 // two accumulator sets its epilogue stages them 32 rows at a time
 // (epi_rows), within the LDS.
@@ -1166,7 +1175,10 @@ constexpr bool has_three_quarter_rows() {
 template <typename T, class C, int NA, int NB, int NACC>
 constexpr int rowgroup_smem_elems() {
   constexpr int a = kernel_smem_elems<C, T, NA, NB, NACC>();
-  if constexpr (has_half_rows<T, C>()) {
+  if constexpr (C::XR == 128) {
+    constexpr int b = rowgroup_smem_elems<T, RowBase<C>, NA, NB, NACC>();
+    return a > b ? a : b;
+  } else if constexpr (has_half_rows<T, C>()) {
     constexpr int b = kernel_smem_elems<QuarterRows<C>, T, NA, NB, NACC>();
     constexpr int c = kernel_smem_elems<HalfRows<C>, T, NA, NB, NACC>();
     constexpr int d = has_three_quarter_rows<C, NACC>()
@@ -1183,6 +1195,14 @@ constexpr int rowgroup_smem_elems() {
 // BM rows (a group's last full tile with its short tail) run as the tall tile.
 template <typename T, class C, int NACC, class F>
 MOE_DEV void with_tile_rows(int mv, F&& body) {
+  if constexpr (C::XR == 128) {
+    if (mv > C::BM + C::BM / 4) {
+      body(C{});
+      return;
+    }
+    with_tile_rows<T, RowBase<C>, NACC>(mv, body);
+    return;
+  }
   if constexpr (has_half_rows<T, C>()) {
     if (mv > C::BM) {
       body(TallRows<C>{});
@@ -1217,7 +1237,10 @@ constexpr bool has_half_cols() { return sizeof(T) == 2 && C::BN == 256; }
 template <typename T, class C, int NA, int NB, int NACC>
 constexpr int rowcol_smem_elems() {
   constexpr int a = rowgroup_smem_elems<T, C, NA, NB, NACC>();
-  if constexpr (has_half_cols<T, C>()) {
+  if constexpr (C::XR == 128) {
+    constexpr int b = rowcol_smem_elems<T, RowBase<C>, NA, NB, NACC>();
+    return a > b ? a : b;
+  } else if constexpr (has_half_cols<T, C>()) {
     constexpr int b = kernel_smem_elems<HalfCols<C>, T, NA, NB, NACC>();
     return a > b ? a : b;
   } else {
@@ -1230,6 +1253,14 @@ constexpr int rowcol_smem_elems() {
 // tiling when that covers the rows, else C.
 template <typename T, class C, class F>
 MOE_DEV void with_tile_shape(int mv, int nv, F&& body) {
+  if constexpr (C::XR == 128) {
+    if (mv > C::BM + C::BM / 4) {  // full width, as the tall tiling
+      body(C{});
+      return;
+    }
+    with_tile_shape<T, RowBase<C>>(mv, nv, body);
+    return;
+  }
   if constexpr (has_half_rows<T, C>()) {
     if (mv > C::BM) {  // full width even when at most BN / 2 columns are valid
       body(TallRows<C>{});
@@ -1269,7 +1300,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_fwd(const T* __restrict__
                                                     T* __restrict__ U, T* __restrict__ A) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 2, 2>()];
   int grp, row0, mv, n0;
-  if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
+  if (!resolve_rows(groups, N, C::AR, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);
   const T* wu = pick(wu_tab, wu_one, grp);
   with_tile_rows<T, C, 2>(mv, [&](auto ct) {
@@ -1302,7 +1333,7 @@ __global__ __launch_bounds__(C::THREADS) void k_down_fwd(const T* __restrict__ A
                                                   int H, T* __restrict__ Y) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
-  if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
+  if (!resolve_rows(groups, H, C::AR, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);
   with_tile_rows<T, C, 1>(mv, [&](auto ct) {
     using CT = decltype(ct);
@@ -1433,7 +1464,7 @@ __global__ __launch_bounds__(C::THREADS) void k_down_dgrad(const T* __restrict__
                                                     T* __restrict__ dG, T* __restrict__ dU) {
   __shared__ __align__(16) T smem[rowcol_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
-  if (!resolve_rows(groups, N, C::BM, C::BN, grp, row0, mv, n0)) return;
+  if (!resolve_rows(groups, N, C::AR, C::BN, grp, row0, mv, n0)) return;
   const T* wd = pick(wd_tab, wd_one, grp);  // [H, N]: element (n, k=h) at wd + h*N + n
   // G and U of a whole 32-column block are requested before its rows are
   // visited; rows outside the tile read zeros (out-of-range offsets).  The
@@ -1492,7 +1523,7 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_dgrad(const T* __restrict
                                                       int I, int H, T* __restrict__ dX) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
-  if (!resolve_rows(groups, H, C::BM, C::BN, grp, row0, mv, n0)) return;
+  if (!resolve_rows(groups, H, C::AR, C::BN, grp, row0, mv, n0)) return;
   const T* wg = pick(wg_tab, wg_one, grp);  // [I, H]: element (n=h, k=i) at wg + i*H + h
   const T* wu = pick(wu_tab, wu_one, grp);
   with_tile_rows<T, C, 1>(mv, [&](auto ct) {

@@ -626,8 +626,8 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
 
 // Index of a row-tile height in kTileBM (the row-grouped tilings use 128
 // (fp32) and 256 (bf16) rows).
-constexpr int tile_slot(int bm) { return bm == 128 ? 0 : 1; }
-static_assert(kNumTileBM == 2, "tile_slot covers the heights of kTileBM");
+constexpr int tile_slot(int bm) { return bm == 128 ? 0 : bm == 256 ? 1 : 2; }
+static_assert(kNumTileBM == 3, "tile_slot covers the heights of kTileBM");
 
 // Blocks of a K-grouped (weight-gradient) launch over `groups` groups or
 // split chunks of an M x N output: each takes 8 * ceil(tiles / 8) blocks.
@@ -739,6 +739,11 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
   }
 }
 
+// Rounds of 384-row tiles over the CUs a row-grouped launch must hold to take
+// them: with fewer, the launch's last partial round costs more than the taller
+// tiles save.
+constexpr int kRows384Rounds = 4;
+
 // Calls f(tiling, row groups, grid(N)) for a row-grouped launch of tiling C
 // with N output columns: the tile prefixes of C::BM, and a grid
 // of the row-tile upper bound TK / BM + E times the column tiles, rounded up
@@ -748,8 +753,27 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
 // traffic, and a half tile that runs apart from its expert's big tiles reads
 // them again (measured: config 2 gate/up forward 296 -> 249 us, config 5
 // row-grouped GEMMs 3-4 % slower).
-template <typename D, class C, class F>
+template <typename D, class C, bool ROWS384 = true, class F>
 void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t TK, F&& f) {
+  if constexpr (ROWS384 && has_half_rows<D, C>()) {
+    // 384-row tiles, the half tiles (at most 192 rows) after the big ones,
+    // when the groups average at least two of them and the launch holds at
+    // least four rounds of them over 256 CUs at six column tiles (I = 1408):
+    // config 3 gate/up forward 1.22 -> 1.11 ms, gate/up input gradient 1.25 ->
+    // 1.22 ms, down forward 0.566 -> 0.55 ms; config 2 (16384 rows) would fill
+    // fewer rounds (its routed GEMMs 8-17 % slower).  The down projection's
+    // input gradient keeps 256-row tiles (ROWS384 = false: config 3 0.86 ->
+    // 0.89 ms with them).
+    using C3 = Rows384<C>;
+    if (TK >= 2 * (int64_t)C3::AR * E && 6 * TK >= (int64_t)kRows384Rounds * 256 * C3::AR) {
+      const int* tp = tprefix_all + kTilePrefixes * tile_slot(C3::AR) * (E + 1);
+      const int mt = ceil_div(TK, C3::AR) + E;
+      static_assert(tall_rows_for(C3::AR) == 0, "384-row tiles take no tails");
+      f(C3{}, RowGroups{offsets, tp, tp + (E + 1), tp + 2 * (E + 1), E, (int)TK, 1, 0},
+        [mt](int N) { return 8 * ceil_div(mt * ceil_div(N, C3::BN), 8); });
+      return;
+    }
+  }
   const int* tp = tprefix_all + kTilePrefixes * tile_slot(C::BM) * (E + 1);
   const int mt = ceil_div(TK, C::BM) + E;
   const int half_last = has_half_rows<D, C>() && TK >= 2 * (int64_t)C::BM * E;
@@ -1121,7 +1145,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   {
     StageTimer tm(p, s, MOE_STAGE_DOWN_DGRAD);
-    with_row_tiling<D, CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
+    with_row_tiling<D, CB, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
       hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(grid(I)), dim3(C::THREADS), 0, s,
                          dY, r, td, nullptr, H, I, 1.0f, G, U, dG, dU);

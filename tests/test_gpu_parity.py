@@ -231,6 +231,35 @@ def test_bf16_tall_tile_parity(spec):
     _check(case, g, o, 1e-2)
 
 
+ROWS384_CASES = [
+    # >= 65536 routed rows and >= 768 rows per expert: the row-grouped GEMMs
+    # run 384-row tiles.  E = 2, k = 2: both experts receive all T rows, so the
+    # last tile of T = 86 * 384 + r rows is a 384-row tile (r = 360), a tall
+    # tile (r = 300), a full tile (r = 220), a three-quarter half tile (r = 160)
+    # or a quarter half tile (r = 60)
+    dict(T=86 * 384 + 360, H=64, E=2, k=2, I=64, S=16),
+    dict(T=86 * 384 + 300, H=72, E=2, k=2, I=72, S=0),
+    dict(T=86 * 384 + 220, H=64, E=2, k=2, I=296, S=0),
+    dict(T=86 * 384 + 160, H=136, E=2, k=2, I=64, S=0),
+    dict(T=86 * 384 + 60, H=64, E=2, k=2, I=88, S=16),
+    # random loads over 8 experts with router bias
+    dict(T=33000, H=64, E=8, k=2, I=64, S=0, bias=True),
+]
+
+
+@pytest.mark.parametrize("spec", ROWS384_CASES)
+def test_bf16_rows384_parity(spec):
+    """Row-grouped GEMMs on 384-row tiles (their tails on the 256-row family)."""
+    spec = dict(spec)
+    bias = zipf_bias(spec["E"], beta=0.3) if spec.pop("bias", False) else None
+    assert spec["T"] * spec["k"] >= 65536 and spec["T"] * spec["k"] >= 768 * spec["E"]
+    case = Case(**spec, dtype="bf16", w_std=0.05, bias=bias)
+    g = gpu_run(case, d_aux=0.01, d_z=0.001)
+    o = oracle_run(case, g["logits"], d_aux=0.01, d_z=0.001)
+    _routing_equal(g, o)
+    _check(case, g, o, 1e-2)
+
+
 SKINNY_CASES = [
     # T <= 64: the forward streams expert weights (skinny kernels); backward
     # runs the tiled kernels on the skinny forward's saved activations
