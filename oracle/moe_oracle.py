@@ -102,6 +102,9 @@ class MoeOracle:
     def __init__(self, cfg, precision=64):
         self.cfg = cfg
         self.dt = np.float64 if precision == 64 else np.float32
+        # kept on the instance: at interpreter exit the module globals may be
+        # gone before the last oracle is collected
+        self._destroy = lib().oracle_destroy
         self.h = lib().oracle_create(ctypes.byref(cfg), precision)
         if not self.h:
             raise ValueError("invalid oracle configuration")
@@ -110,7 +113,7 @@ class MoeOracle:
 
     def __del__(self):
         if getattr(self, "h", None):
-            lib().oracle_destroy(self.h)
+            self._destroy(self.h)
             self.h = None
 
     def _c(self, a):

@@ -703,6 +703,30 @@ struct State {
 
 // Shared expert forward over all T tokens on stream ss: G, U (when kept), A,
 // and the down projection into sY when sY is not null.
+// Calls f(tiling, grid) for a dense (shared-expert) launch of tiling C over
+// T rows and N columns: C, or its 384-row tiles when those fill fewer whole
+// rounds of 256 CUs, a 384-row tile counted at kDense384Cost tenths of a
+// 256-row one (a k-tile brings 25 % more operand rows for 50 % more MFMA
+// work).  The last row tile runs as the shortest tiling that covers it.
+#ifndef DENSE384_COST
+#define DENSE384_COST 14
+#endif
+constexpr int kDense384Cost = DENSE384_COST;
+template <typename D, class C, class F>
+void with_dense_tiling(int T, int N, F&& f) {
+  const int64_t nN = ceil_div(N, C::BN);
+  if constexpr (has_half_rows<D, C>()) {
+    using C3 = Rows384<C>;
+    const int64_t r256 = ceil_div(ceil_div(T, C::BM) * nN, (int64_t)256);
+    const int64_t r384 = ceil_div(ceil_div(T, C3::AR) * nN, (int64_t)256);
+    if (kDense384Cost * r384 < 10 * r256) {
+      f(C3{}, (int)(ceil_div(T, C3::AR) * nN));
+      return;
+    }
+  }
+  f(C{}, (int)(ceil_div(T, C::BM) * nN));
+}
+
 template <typename D>
 void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weights* w, D* sG,
                 D* sU, D* sA, D* sY) {
@@ -730,12 +754,18 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
                          nullptr, nullptr, S, H, (bf16_t*)sY, nullptr, nullptr);
   } else {
     const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0, 0};
-    hipLaunchKernelGGL((k_gateup_fwd<D, false>), dim3(ceil_div(T, CG::BM) * ceil_div(S, CG::BN)),
-                       dim3(CG::THREADS), 0, ss, x, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                       (const D*)w->shared_up, H, S, sG, sU, sA);
+    with_dense_tiling<D, CG>(T, S, [&](auto c, int grid) {
+      using C = decltype(c);
+      hipLaunchKernelGGL((k_gateup_fwd<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, x, dense,
+                         nullptr, (const D*)w->shared_gate, nullptr, (const D*)w->shared_up, H, S,
+                         sG, sU, sA);
+    });
     if (sY)
-      hipLaunchKernelGGL((k_down_fwd<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)),
-                         dim3(CB::THREADS), 0, ss, sA, dense, nullptr, (const D*)w->shared_down, S, H, sY);
+      with_dense_tiling<D, CB>(T, H, [&](auto c, int grid) {
+        using C = decltype(c);
+        hipLaunchKernelGGL((k_down_fwd<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, sA, dense,
+                           nullptr, (const D*)w->shared_down, S, H, sY);
+      });
   }
 }
 
@@ -1083,10 +1113,17 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     dxs = (D*)(ws + W.dxs);
     const float sc = c.shared_expert_scale;
     const RowGroups dense{nullptr, nullptr, nullptr, nullptr, 1, T, 0, 0};
-    hipLaunchKernelGGL((k_down_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(S, CB::BN)), dim3(CB::THREADS), 0, ss, dout, dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU,
-                       sdG, sdU);
-    hipLaunchKernelGGL((k_gateup_dgrad<D, false>), dim3(ceil_div(T, CB::BM) * ceil_div(H, CB::BN)), dim3(CB::THREADS), 0, ss, sdG, sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                       (const D*)w->shared_up, S, H, dxs);
+    with_dense_tiling<D, CB>(T, S, [&](auto c, int grid) {
+      using C = decltype(c);
+      hipLaunchKernelGGL((k_down_dgrad<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, dout,
+                         dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU, sdG, sdU);
+    });
+    with_dense_tiling<D, CB>(T, H, [&](auto c, int grid) {
+      using C = decltype(c);
+      hipLaunchKernelGGL((k_gateup_dgrad<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, sdG,
+                         sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
+                         (const D*)w->shared_up, S, H, dxs);
+    });
     if (ss != s) {
       HIP_TRY(hipEventRecord(p->sdx, ss));
       wait_sdx = true;

@@ -260,6 +260,39 @@ def test_bf16_rows384_parity(spec):
     _check(case, g, o, 1e-2)
 
 
+DENSE384_CASES = [
+    # The shared expert's dense GEMMs over T tokens and S = 2816 columns (11
+    # tiles of 256, 22 of 128): 25-26 row tiles of 256 rows take two rounds of
+    # 256 CUs (the gate/up forward three), 17 of 384 rows one (two), so the
+    # gate/up forward and the down projection's input gradient run 384-row
+    # tiles.  Their last row tile has 56 rows (a quarter tile) or 356 (a
+    # 384-row tile with 28 padding rows).
+    dict(T=6200, H=64, E=2, k=1, I=64, S=2816),
+    dict(T=6500, H=72, E=4, k=2, I=64, S=2816),
+    # S = 1408 (six tiles of 256, the last half wide): only the down
+    # projection's input gradient switches (43 -> 29 row tiles)
+    dict(T=11000, H=64, E=2, k=1, I=64, S=1408),
+]
+
+
+def _dense_rounds(T, N, bm, bn, cus=256):
+    return -(-(-(-T // bm) * -(-N // bn)) // cus)
+
+
+@pytest.mark.parametrize("spec", DENSE384_CASES)
+def test_bf16_dense384_shared_parity(spec):
+    """The shared expert's dense GEMMs on 384-row tiles (a 384-row tile is
+    chosen when it fills fewer rounds of the CUs at 1.4 times the cost of a
+    256-row tile; the last row tile runs on the 256-row family)."""
+    T, S = spec["T"], spec["S"]
+    assert 1.4 * _dense_rounds(T, S, 384, 256) < _dense_rounds(T, S, 256, 256)
+    case = Case(**spec, dtype="bf16", w_std=0.05)
+    g = gpu_run(case, d_aux=0.01, d_z=0.001)
+    o = oracle_run(case, g["logits"], d_aux=0.01, d_z=0.001)
+    _routing_equal(g, o)
+    _check(case, g, o, 1e-2)
+
+
 SKINNY_CASES = [
     # T <= 64: the forward streams expert weights (skinny kernels); backward
     # runs the tiled kernels on the skinny forward's saved activations
