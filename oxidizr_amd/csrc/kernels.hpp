@@ -93,6 +93,16 @@ MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
                                                 __builtin_bit_cast(bf16x8_t, b), acc, 0, 0, 0);
 }
+MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b, bf16_t) { mfma16(acc, a, b); }
+// fp32 operands, four 16 x 16 x 4 MFMAs: lane l supplies the four consecutive k
+// 4 (l / 16) + c (+ 16 q per load) of a-row and b-row l % 16, component c to
+// step c, so the four lane groups cover 16 k per load; same output layout.
+MOE_DEV void mfma16(f32x4& acc, u32x4 a, u32x4 b, float) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.x), __uint_as_float(b.x), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.y), __uint_as_float(b.y), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.z), __uint_as_float(b.z), acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a.w), __uint_as_float(b.w), acc, 0, 0, 0);
+}
 
 // Output-tile order.  Workgroup ids are first made contiguous per XCD
 // (xcd_slot); consecutive ids then walk GM row-tiles down a tile column
@@ -486,28 +496,29 @@ __global__ __launch_bounds__(256) void k_route(const float* __restrict__ logits,
 }
 
 // ------------------------------------------------------------------ fused router
-// Router GEMM, softmax, log-sum-exp and top-k in one launch (bf16, up to
-// kFusedRouterMaxExperts experts).  A workgroup of kRouterWaves waves owns 16
-// tokens and every expert (NEB = ceil(E / 16) blocks of 16): each wave takes
-// every kRouterWaves-th kFusedRouterChunk-wide k-chunk of the hidden dimension
-// and multiplies its 16 token rows with the NEB router-row blocks
-// (v_mfma_f32_16x16x32_bf16), the partial sums are added through LDS in wave
-// order, and each of the 16 waves then routes one token with route_row (the
-// arithmetic of k_route) from the logits row staged in LDS.  128-wide chunks
+// Router GEMM, softmax, log-sum-exp and top-k in one launch (bf16 or fp32, up
+// to kFusedRouterMaxExperts experts).  A workgroup of kRouterWaves waves owns
+// 16 tokens and every expert (NEB = ceil(E / 16) blocks of 16): each wave
+// takes every kRouterWaves-th k-chunk of kFusedRouterChunkBytes per row of the
+// hidden dimension and multiplies its 16 token rows with the NEB router-row
+// blocks (v_mfma_f32_16x16x32_bf16, or four v_mfma_f32_16x16x4f32 per load
+// for fp32), the partial sums are added through LDS in wave order, and each
+// of the 16 waves then routes one token with route_row (the arithmetic of
+// k_route) from the logits row staged in LDS.  256-byte chunks (128 bf16)
 // give every wave a chunk at H = 2048 and keep the loads in flight within
-// 64 VGPRs, so two workgroups share a CU (256-wide chunks: half the waves
+// 64 VGPRs, so two workgroups share a CU (512-byte chunks: half the waves
 // idle at H = 2048, 72 VGPRs, one workgroup per CU, two rounds of
 // workgroups for 8192 tokens).
 constexpr int kFusedRouterMaxExperts = 64;
-constexpr int kFusedRouterChunk = 128;
+constexpr int kFusedRouterChunkBytes = 256;
 // The workgroup also writes what the dispatch and the losses need from its 16
 // tokens: the expert histogram of their k choices (group_hist[b][e], an
 // integer LDS histogram) and the column sums of their probabilities
 // (prob_part[b][e], tokens added in order), so that k_scan over the 16-token
 // groups and k_colsum_final finish the counts, offsets and P.
-template <int NEB>
+template <typename T, int NEB>
 __global__ __launch_bounds__(64 * kRouterWaves) __attribute__((amdgpu_waves_per_eu(8))) void k_router_route(
-    const bf16_t* __restrict__ x, const bf16_t* __restrict__ wr, const float* __restrict__ bias,
+    const T* __restrict__ x, const T* __restrict__ wr, const float* __restrict__ bias,
     int Tn, int H, int E, int k, float tau, int norm, float* __restrict__ logits,
     float* __restrict__ probs, float* __restrict__ lse, int* __restrict__ idx,
     float* __restrict__ w, int* __restrict__ group_hist, float* __restrict__ prob_part) {
@@ -520,30 +531,33 @@ __global__ __launch_bounds__(64 * kRouterWaves) __attribute__((amdgpu_waves_per_
   const int wave = uni(threadIdx.x >> 6), lane = threadIdx.x & 63;
   const int g = lane >> 4, rl = lane & 15;
   const int ntok = min(16, Tn - t0);
-  const rsrc_t rx = make_rsrc(x + (int64_t)t0 * H, (uint32_t)((int64_t)ntok * H * 2));
-  const rsrc_t rw = make_rsrc(wr, (uint32_t)((int64_t)E * H * 2));
-  const uint32_t vx = (uint32_t)((rl * H + 8 * g) * 2);
+  constexpr int B = (int)sizeof(T);
+  constexpr int V = 16 / B;                           // elements per 16-byte load
+  constexpr int CH = kFusedRouterChunkBytes / B;      // chunk elements per row
+  constexpr int NQ = CH / (4 * V);                    // loads per chunk: 4 lane groups x V
+  const rsrc_t rx = make_rsrc(x + (int64_t)t0 * H, (uint32_t)((int64_t)ntok * H * B));
+  const rsrc_t rw = make_rsrc(wr, (uint32_t)((int64_t)E * H * B));
+  const uint32_t vx = (uint32_t)((rl * H + V * g) * B);
   f32x4 acc[NEB];
 #pragma unroll
   for (int b = 0; b < NEB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  for (int kc = wave; kc * kFusedRouterChunk < H; kc += kRouterWaves) {
-    constexpr int NQ = kFusedRouterChunk / 32;
-    const uint32_t soff = (uint32_t)kc * (2 * kFusedRouterChunk);
+  for (int kc = wave; kc * CH < H; kc += kRouterWaves) {
+    const uint32_t soff = (uint32_t)kc * kFusedRouterChunkBytes;
     u32x4 xa[NQ], wa[NEB][NQ];
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
-      const bool kin = kc * kFusedRouterChunk + 32 * q + 8 * g < H;
+      const bool kin = kc * CH + 4 * V * q + V * g < H;
       xa[q] = buf_ld16(rx, kin ? vx + 64 * q : kOobOffset, soff);
 #pragma unroll
       for (int b = 0; b < NEB; ++b) {
-        const uint32_t vw = (uint32_t)(((b * 16 + rl) * H + 8 * g) * 2);
+        const uint32_t vw = (uint32_t)(((b * 16 + rl) * H + V * g) * B);
         wa[b][q] = buf_ld16(rw, kin && b * 16 + rl < E ? vw + 64 * q : kOobOffset, soff);
       }
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q)
 #pragma unroll
-      for (int b = 0; b < NEB; ++b) mfma16(acc[b], xa[q], wa[b][q]);
+      for (int b = 0; b < NEB; ++b) mfma16(acc[b], xa[q], wa[b][q], T());
   }
 #pragma unroll
   for (int b = 0; b < NEB; ++b) red[wave][b][lane] = acc[b];

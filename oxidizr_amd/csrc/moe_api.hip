@@ -90,15 +90,17 @@ struct WsLayout {
 int elt_size(int dtype) { return dtype == MOE_DTYPE_F32 ? 4 : 2; }
 
 // The fused router kernel (router GEMM + routing + the 16-token groups'
-// histograms and probability sums) applies to bf16 plans with up to
+// histograms and probability sums) applies to plans (bf16 or fp32) with up to
 // kFusedRouterMaxExperts experts and more than kRouteSmallTokens tokens (the
 // small-token path keeps k_router_small, whose 16 x 16 blocks spread a few
 // tokens over more workgroups).  With more experts a workgroup that owns every
 // expert of its tokens re-reads the whole router weight per 16 tokens; there
-// the tiled router GEMM and k_route stay separate.
+// the tiled router GEMM and k_route stay separate.  fp32 (config 1: T = 1024,
+// H = 384, E = 8): router, route and dispatch stages 31 + 14 + 22 us as the
+// tiled GEMM (8 workgroups), k_route, k_hist, k_scan and k_scatter.
 bool fused_router(const moe_config& c, int64_t T) {
-  return c.dtype == MOE_DTYPE_BF16 && c.num_experts <= kFusedRouterMaxExperts &&
-         T > kRouteSmallTokens;
+  return (c.dtype == MOE_DTYPE_BF16 || c.dtype == MOE_DTYPE_F32) &&
+         c.num_experts <= kFusedRouterMaxExperts && T > kRouteSmallTokens;
 }
 // Chunks of H the tiled router GEMM splits its k-loop into (k_router_logits_split):
 // one per 1792 columns from H = 3584 up (config 5: 7168 -> 4 chunks of 28
@@ -536,11 +538,11 @@ void launch_route(hipStream_t s, int grid, const float* logits, int T, int E, in
 // weight-gradient stream, forked through *pjoin; the caller joins it before
 // reading P.
 
-template <int NEB>
-void launch_router_route(hipStream_t s, int T, const bf16_t* x, const bf16_t* wr, const float* b,
+template <int NEB, typename D>
+void launch_router_route(hipStream_t s, int T, const D* x, const D* wr, const float* b,
                          int H, int E, int k, float tau, int norm, float* logits, float* probs,
                          float* lse, int* idx, float* w, int* ghist, float* gpart) {
-  hipLaunchKernelGGL((k_router_route<NEB>), dim3(route_groups(T)), dim3(64 * kRouterWaves), 0, s,
+  hipLaunchKernelGGL((k_router_route<D, NEB>), dim3(route_groups(T)), dim3(64 * kRouterWaves), 0, s,
                      x, wr, b, T, H, E, k, tau, norm, logits, probs, lse, idx, w, ghist, gpart);
 }
 
@@ -935,19 +937,19 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     StageTimer tm(p, s, MOE_STAGE_ROUTER_GEMM);
     const RouterPath rp = router_path(c, T64);
     if (rp == RouterPath::Fused) {  // router GEMM, softmax, lse and top-k in one launch
-      const bf16_t* xb = (const bf16_t*)x;
-      const bf16_t* wrb = (const bf16_t*)w->router;
+      const D* xb = x;
+      const D* wrb = (const D*)w->router;
       const float* rbias = c.has_router_bias ? w->router_bias : nullptr;
       const float tau = c.router_temperature;
       const int nt = c.norm_topk_prob;
       int* gh = (int*)(ws + W.ghist);
       float* gp = (float*)(ws + W.gpart);
       if (E <= 16)
-        launch_router_route<1>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
+        launch_router_route<1, D>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
       else if (E <= 32)
-        launch_router_route<2>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
+        launch_router_route<2, D>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
       else
-        launch_router_route<4>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
+        launch_router_route<4, D>(s, T, xb, wrb, rbias, H, E, k, tau, nt, st.logits, st.probs, st.lse, st.idx, st.w, gh, gp);
     } else if (rp == RouterPath::Small) {
       hipLaunchKernelGGL(k_router_small, dim3(ceil_div(E, 16) * ceil_div(T, 16)),
                          dim3(64 * kRouterWaves), 0, s, (const bf16_t*)x,

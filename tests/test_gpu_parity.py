@@ -105,7 +105,8 @@ FP32_CASES = [
     dict(T=1024, H=384, E=8, k=2, I=1024, S=0),     # BASELINE config 1 (fp32, CPU-runnable)
     dict(T=33, H=136, E=12, k=12, I=16, S=0),       # k == E: every expert selected
     dict(T=150, H=64, E=10, k=6, I=32, S=16),       # 4 < k <= 8 (dx gathers sized for k <= 8)
-    dict(T=130, H=3592, E=6, k=2, I=32, S=0, bias=True),  # router k-loop split in two chunks
+    dict(T=130, H=3592, E=6, k=2, I=32, S=0, bias=True),  # fused router over 57 k-chunks
+    dict(T=130, H=3592, E=72, k=2, I=16, S=0, bias=True),  # E > 64: router k-loop split in two chunks
     dict(T=200, H=64, E=1020, k=5, I=16, S=16),     # E not a multiple of 8, most experts empty
     dict(T=100, H=64, E=4, k=1, I=32, S=0),         # top-1 routing
 ]
