@@ -629,7 +629,7 @@ moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, cha
 
 // Index of a row-tile height in kTileBM (the row-grouped tilings use 128
 // (fp32) and 256 (bf16) rows).
-constexpr int tile_slot(int bm) { return bm == 128 ? 0 : bm == 256 ? 1 : 2; }
+constexpr int tile_slot(int bm) { return bm == kF32RowTile ? 0 : bm == 256 ? 1 : 2; }
 static_assert(kNumTileBM == 3, "tile_slot covers the heights of kTileBM");
 
 // Blocks of a K-grouped (weight-gradient) launch over `groups` groups or
