@@ -50,14 +50,16 @@ template <> struct Tilings<bf16_t> {
 // weight-gradient pair they measured no faster.  64-row tiles for the
 // row-grouped GEMMs double the workgroups again (~256 rows per expert: gate/up
 // input gradient 86 -> 55 us, down forward 40 -> 27 us, step 0.321 -> 0.297
-// ms).
+// ms); the weight-gradient pair on 64 x 128 tiles as well (gate/up weight
+// gradient 55 -> 48 us, step 0.300 -> 0.292 ms), and the router GEMMs and the
+// input gradient dx (dx 16.8 -> 11.8 us, step 0.292 -> 0.288 ms).
 constexpr int kF32RowTile = 64;
 template <> struct Tilings<float> {
-  using Router = Tiling<float, 128, 128, 32>;
+  using Router = Tiling<float, 64, 128, 32>;
   using RouterNarrow = Router;
   using GateUp = Tiling<float, kF32RowTile, 64, 32>;
   using Big = Tiling<float, kF32RowTile, 64, 32>;
-  using WgradPair = Tiling<float, 128, 128, 32>;
+  using WgradPair = Tiling<float, 64, 128, 32>;
 };
 
 // Row-grouped problems: groups split the M dimension (permuted token rows).
