@@ -37,8 +37,12 @@ template <typename T> struct Tilings;
 // RouterNarrow: 64-row router tiles with four stages, for launches whose
 // 128-row grid would leave CUs idle (config 5: 128 -> 256 workgroups, router
 // GEMM 120.7 -> 105 us; two stages 107.5 us).
+// RouterDx: the input gradient dx (k_router_dgrad): 64-row tiles give its
+// gather-sum twice the workgroups (config 2 43 -> 38 us, config 3 184 -> 176
+// us, config 5 unchanged), where the router GEMM itself is faster on 128 rows.
 template <> struct Tilings<bf16_t> {
   using Router = Tiling<bf16_t, 128, 128, 64>;
+  using RouterDx = Tiling<bf16_t, 64, 128, 64>;
   using RouterNarrow = Tiling<bf16_t, 64, 128, 64, 4, 4>;
   using GateUp = Tiling<bf16_t, 256, 128, 64, 2, 2, 8>;
   using Big = Tiling<bf16_t, 256, 256, 64, 2, 2, 8>;
@@ -56,6 +60,7 @@ template <> struct Tilings<bf16_t> {
 constexpr int kF32RowTile = 64;
 template <> struct Tilings<float> {
   using Router = Tiling<float, 64, 128, 32>;
+  using RouterDx = Router;
   using RouterNarrow = Router;
   using GateUp = Tiling<float, kF32RowTile, 64, 32>;
   using Big = Tiling<float, kF32RowTile, 64, 32>;
@@ -1762,7 +1767,7 @@ __global__ __launch_bounds__(256) void k_router_bwd(
 // accumulator, then the k gathered rows in slot order, then dxs.
 template <typename T>
 constexpr int dgrad_smem_elems() {
-  using C = typename Tilings<T>::Router;
+  using C = typename Tilings<T>::RouterDx;
   constexpr int a = kernel_smem_elems<C, T, 1, 1, 1>();
   constexpr int b = C::BM * (C::BN + 4) * 4 / (int)sizeof(T);
   return a > b ? a : b;
@@ -1774,7 +1779,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
                                                       const int* __restrict__ inv_perm, int k,
                                                       const T* __restrict__ dxs,
                                                       T* __restrict__ dx) {
-  using C = typename Tilings<T>::Router;
+  using C = typename Tilings<T>::RouterDx;
   static_assert(C::THREADS == 256 && C::BN == 128, "16 units of 8 columns per row, 16 rows per pass");
   __shared__ __align__(16) T smem[dgrad_smem_elems<T>()];
   // row-major tile order: the column tiles of one row block run together, so

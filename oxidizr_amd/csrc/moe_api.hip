@@ -1246,7 +1246,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   if (wait_sdx) HIP_TRY(hipStreamWaitEvent(s, p->sdx, 0));
   {
     StageTimer tm(p, s, MOE_STAGE_DX);
-    const dim3 grid(ceil_div(T, CR::BM) * ceil_div(H, CR::BN));
+    using CX = typename Tilings<D>::RouterDx;
+    const dim3 grid(ceil_div(T, CX::BM) * ceil_div(H, CX::BN));
     const D* wr = (const D*)w->router;
     if (k <= 2)
       hipLaunchKernelGGL((k_router_dgrad<D, 2>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
