@@ -711,10 +711,7 @@ struct State {
 // rounds of 256 CUs, a 384-row tile counted at kDense384Cost tenths of a
 // 256-row one (a k-tile brings 25 % more operand rows for 50 % more MFMA
 // work).  The last row tile runs as the shortest tiling that covers it.
-#ifndef DENSE384_COST
-#define DENSE384_COST 14
-#endif
-constexpr int kDense384Cost = DENSE384_COST;
+constexpr int kDense384Cost = 14;
 template <typename D, class C, class F>
 void with_dense_tiling(int T, int N, F&& f) {
   const int64_t nN = ceil_div(N, C::BN);
