@@ -412,11 +412,14 @@ def measure(args, config, steps, warmup, extras=True):
         "router_gemm": T * H * b + E * H * b + T * E * 4,
         "route": 3 * T * E * 4 + T * 4 + TK * 8,
         "dispatch": 2 * TK * 4 + TK * 8 + 2 * E * 4,
-        "gather": T * H * b + TK * H * b + TK * 4,
         "combine_fwd": TK * H * b + (T * H * b if S else 0) + TK * 8 + T * H * b,
     }
     if wl.backward:
-        stage_bytes["combine_bwd"] = T * H * b + 2 * TK * H * b + TK * 8 + TK * 4
+        # the backward's weighted token rows (x read once, T*k rows written,
+        # inv_perm and weights read); the forward keeps no permuted copy
+        stage_bytes["gather"] = T * H * b + TK * H * b + TK * 8
+        # weighted d_out rows for the down weight gradient
+        stage_bytes["combine_bwd"] = T * H * b + TK * H * b + TK * 8
     hbm_stages = {}
     for name, nbytes in stage_bytes.items():
         if stages.get(name):

@@ -221,11 +221,14 @@ typedef enum {
   MOE_SAVED_PERM,         /* int32 [T*k]: expert-major position -> t*k + j */
   MOE_SAVED_INV_PERM,     /* int32 [T*k]: t*k + j -> position */
   MOE_SAVED_MEAN_PROB,    /* fp32 [E]: P_e = mean_t probs[t, e] */
-  MOE_SAVED_X_PERM,       /* dtype [T*k, H] */
+  MOE_SAVED_X_PERM,       /* 0 bytes: the expert GEMMs read each assignment's token
+                             row of x through the permutation (no permuted copy) */
   MOE_SAVED_GATE_ACT,     /* dtype [T*k, I]: x W_g^T */
   MOE_SAVED_UP_ACT,       /* dtype [T*k, I]: x W_u^T */
   MOE_SAVED_SWIGLU,       /* dtype [T*k, I]: silu(gate) * up */
-  MOE_SAVED_EXPERT_OUT,   /* dtype [T*k, H]: per-assignment expert output */
+  MOE_SAVED_EXPERT_OUT,   /* dtype [T*k, H]: per-assignment expert output; 0 bytes in
+                             a training forward's `saved` (the backward does not
+                             read it), present in the forward-only state */
   MOE_SAVED_RSTD,         /* fp32 [T]: 1 / RMS of h (fused_block plans only) */
   MOE_SAVED_NORM_X,       /* dtype [T, H]: RMSNorm(h), the layer input (fused_block only) */
   MOE_SAVED_NUM_FIELDS

@@ -72,13 +72,31 @@ struct Tiling {
 // points refuse token counts whose largest such extent (T x max(H, I, S, E)
 // elements, a group holding at most T rows) reaches 2^31 bytes
 // (moe_check_tokens), and plans whose weight matrices do.
+//
+// Gathered K-contiguous operand (the main loop's AG flag): tile row r < rows_valid
+// is row rows[r] / rdiv of the src_rows x ld matrix at base, so a tile reads
+// token rows of an unpermuted matrix in expert order (rows: the permutation,
+// entries t * k + j; rdiv = k) without a permuted copy.  Each lane reads its
+// rows' indices once, before the k-loop; an index outside [0, src_rows * rdiv)
+// reads zeros.
 template <typename T>
 struct OpDesc {
   const T* base;
   int64_t ld;
   int rows_valid;
   int k_valid;
+  const int* rows = nullptr;
+  int src_rows = 0;
+  int rdiv = 1;
 };
+// Byte offset of gathered row r's k-column kcol, or kOobOffset.
+template <typename T>
+MOE_DEV uint32_t gathered_row_offset(const OpDesc<T>& d, int r, int kcol) {
+  if (r >= d.rows_valid) return kOobOffset;
+  const int p = d.rows[r];
+  if ((unsigned)p >= (unsigned)d.src_rows * (unsigned)d.rdiv) return kOobOffset;
+  return (uint32_t)(((int64_t)(p / d.rdiv) * d.ld + kcol) * (int64_t)sizeof(T));
+}
 
 MOE_DEV void mfma_frag(f32x16& acc, u32x4 bt, u32x4 at, bf16_t) {
   acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, bt),
@@ -115,11 +133,11 @@ MOE_DEV void transpose_vv(const u32x4 (&in)[4], u32x4 (&out)[4], float) {
 // readable extent, so out-of-range rows and the K tail come back as zero from
 // the hardware (no per-load branches), the tile base sits in scalar registers
 // and each load needs one 32-bit offset register.
-template <class C, typename T, int R, bool TRANS>
+template <class C, typename T, int R, bool TRANS, bool G = false>
 struct Stager;
 
-template <class C, typename T, int R>
-struct Stager<C, T, R, false> {
+template <class C, typename T, int R, bool G>
+struct Stager<C, T, R, false, G> {
   static constexpr int KV = C::BK / C::V;              // vectors per row
   static constexpr int TOTAL = R * KV;
   static_assert(TOTAL % C::THREADS == 0, "tile rows must cover the workgroup");
@@ -129,9 +147,11 @@ struct Stager<C, T, R, false> {
   rsrc_t rs[2];                                        // one per K segment
   int k_valid[2];
   uint32_t voff, step;
+  uint32_t vrow[G ? PER : 1];                          // gathered: each load's row offset
   int kcol;
   MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
-    const int64_t limit = (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
+    const int64_t limit = G ? (int64_t)d.src_rows * d.ld
+                            : (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
     return make_rsrc(d.base, (uint32_t)(limit * (int64_t)sizeof(T)));
   }
   MOE_DEV void init(const OpDesc<T>& d, int tid) {
@@ -140,6 +160,12 @@ struct Stager<C, T, R, false> {
     kcol = (tid % KV) * C::V;
     voff = (uint32_t)(((tid / KV) * d.ld + kcol) * (int64_t)sizeof(T));
     step = (uint32_t)(ROWS_STEP * d.ld * (int64_t)sizeof(T));
+    if constexpr (G) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        vrow[i] = gathered_row_offset(d, tid / KV + i * ROWS_STEP, kcol);
+      }
+    }
   }
   // Second K segment: same ld and rows as the first.
   MOE_DEV void init_second(const OpDesc<T>& d) {
@@ -150,7 +176,8 @@ struct Stager<C, T, R, false> {
     const uint32_t soff = (uint32_t)k0 * sizeof(T);
     const bool kin = k0 + kcol < k_valid[seg];
 #pragma unroll
-    for (int i = 0; i < PER; ++i) r[i] = buf_ld16(rs[seg], kin ? voff + i * step : kOobOffset, soff);
+    for (int i = 0; i < PER; ++i)
+      r[i] = buf_ld16(rs[seg], kin ? (G ? vrow[i] : voff + i * step) : kOobOffset, soff);
   }
   MOE_DEV void store(T* s, int tid) const {
 #pragma unroll
@@ -241,7 +268,7 @@ typedef __attribute__((address_space(3))) i16x4_t lds_i16x4_t;
 MOE_DEV int nt_swz(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 MOE_DEV int tr_swz(int k) { return (k & 3) << 2; }
 
-template <class C, typename T, int R>
+template <class C, typename T, int R, bool G = false>
 struct DmaStager {
   static constexpr int KV = C::BK / C::V;    // 16-byte slots per row
   static_assert(KV == 8 || KV == 4, "rows of 8 or 4 slots");
@@ -254,9 +281,11 @@ struct DmaStager {
   rsrc_t rs[2];                              // one per K segment
   int k_valid[2];
   uint32_t voff, step;
+  uint32_t vrow[G ? PER : 1];                // gathered: each instruction's row offset
   int kcol;
   MOE_DEV static rsrc_t rsrc_of(const OpDesc<T>& d) {
-    const int64_t limit = (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
+    const int64_t limit = G ? (int64_t)d.src_rows * d.ld
+                            : (int64_t)(d.rows_valid - 1) * d.ld + d.k_valid;
     return make_rsrc(d.base, (uint32_t)(limit * (int64_t)sizeof(T)));
   }
   MOE_DEV void init(const OpDesc<T>& d, int tid) {
@@ -267,6 +296,12 @@ struct DmaStager {
     kcol = ((lane % KV) ^ swz(row)) * C::V;
     voff = (uint32_t)((row * d.ld + kcol) * (int64_t)sizeof(T));
     step = (uint32_t)(C::NW * RPI * d.ld * (int64_t)sizeof(T));
+    if constexpr (G) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        vrow[i] = gathered_row_offset(d, row + i * C::NW * RPI, kcol);
+      }
+    }
   }
   MOE_DEV void init_second(const OpDesc<T>& d) {  // same ld and rows as the first
     rs[1] = rsrc_of(d);
@@ -281,7 +316,7 @@ struct DmaStager {
     for (int i = 0; i < PER; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           rs[seg], (lds_void_t*)(tile + (i * C::NW * RPI + wave * RPI) * C::BK), 16,
-          kin ? voff + i * step : kOobOffset, soff, 0, 0);
+          kin ? (G ? vrow[i] : voff + i * step) : kOobOffset, soff, 0, 0);
   }
   MOE_DEV static u32x4 frag(const T* tile, int row, int kv) {
     return *reinterpret_cast<const u32x4*>(tile + row * C::BK + ((kv ^ swz(row)) * C::V));
@@ -374,7 +409,7 @@ struct DmaStagerT {
 // than two stages at each k-tile.
 MOE_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
+template <class C, typename T, bool A_T, bool B_T, int NA, int NB, bool AG = false>
 MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
                           f32x16 (&xacc)[NA * NB][C::XTN], const OpDesc<T> (&a)[NA],
                           const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2,
@@ -384,7 +419,8 @@ MOE_DEV void mainloop_dma(f32x16 (&acc)[NA * NB][C::TN][C::TM],
   constexpr int NST = C::NST;
   constexpr bool TALL = C::XR > 0;
   static_assert(!TALL || !A_T, "tall tiles take a K-contiguous A operand");
-  using SA = typename std::conditional<A_T, DmaStagerT<C, T, C::AR>, DmaStager<C, T, C::AR>>::type;
+  static_assert(!AG || !A_T, "gathered rows: K-contiguous A");
+  using SA = typename std::conditional<A_T, DmaStagerT<C, T, C::AR>, DmaStager<C, T, C::AR, AG>>::type;
   using SB = typename std::conditional<B_T, DmaStagerT<C, T, C::BN>, DmaStager<C, T, C::BN>>::type;
   // DMA instructions one wave issues per k-tile
   constexpr int IPT = NA * SA::PER + NB * SB::PER;
@@ -589,7 +625,7 @@ constexpr int smem_elems() {
 //
 // An optional second K segment (a2, b2, K2: same ld and rows as a and b)
 // continues the same pipeline, so sum_k A1 B1 + sum_k A2 B2 runs as one loop.
-template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
+template <class C, typename T, bool A_T, bool B_T, int NA, int NB, bool AG = false>
 MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)[NA],
                       const OpDesc<T> (&b)[NB], int K, T* smem, const OpDesc<T>* a2 = nullptr,
                       const OpDesc<T>* b2 = nullptr, int K2 = 0) {
@@ -599,7 +635,7 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
   if constexpr (sizeof(T) == 2 || (!A_T && !B_T)) {
     static_assert(C::NST * (NA * C::BM + NB * C::BN) * C::BK <= smem_elems<C, NA, NB>(), "LDS");
     f32x16 unused[NA * NB][C::XTN];
-    mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, unused, a, b, K, smem, a2, b2, K2);
+    mainloop_dma<C, T, A_T, B_T, NA, NB, AG>(acc, unused, a, b, K, smem, a2, b2, K2);
     return;
   }
   constexpr int STAGE = stage_elems<C, NA, NB>();
@@ -607,7 +643,8 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave / C::WGN, wn = wave % C::WGN;
-  Stager<C, T, C::BM, A_T> sa[NA];
+  static_assert(!AG || !A_T, "gathered rows: K-contiguous A");
+  Stager<C, T, C::BM, A_T, AG> sa[NA];
   Stager<C, T, C::BN, B_T> sb[NB];
   const int nk1 = (K + C::BK - 1) / C::BK;
   const int nk = nk1 + (K2 > 0 ? (K2 + C::BK - 1) / C::BK : 0);
@@ -697,15 +734,15 @@ MOE_DEV void mainloop(f32x16 (&acc)[NA * NB][C::TN][C::TM], const OpDesc<T> (&a)
 
 // mainloop for a row tile that may be tall (C::XR > 0, bf16): xacc holds the
 // wave's extra blocks (unused when C::XR == 0).
-template <class C, typename T, bool A_T, bool B_T, int NA, int NB>
+template <class C, typename T, bool A_T, bool B_T, int NA, int NB, bool AG = false>
 MOE_DEV void mainloop_x(f32x16 (&acc)[NA * NB][C::TN][C::TM], f32x16 (&xacc)[NA * NB][C::XTN],
                         const OpDesc<T> (&a)[NA], const OpDesc<T> (&b)[NB], int K, T* smem,
                         const OpDesc<T>* a2 = nullptr, const OpDesc<T>* b2 = nullptr,
                         int K2 = 0) {
   if constexpr (C::XR > 0)
-    mainloop_dma<C, T, A_T, B_T, NA, NB>(acc, xacc, a, b, K, smem, a2, b2, K2);
+    mainloop_dma<C, T, A_T, B_T, NA, NB, AG>(acc, xacc, a, b, K, smem, a2, b2, K2);
   else
-    mainloop<C, T, A_T, B_T, NA, NB>(acc, a, b, K, smem, a2, b2, K2);
+    mainloop<C, T, A_T, B_T, NA, NB, AG>(acc, a, b, K, smem, a2, b2, K2);
 }
 
 template <class C, int NACC>
@@ -784,17 +821,18 @@ constexpr int kernel_smem_elems() {
 // outputs per lane (16-byte bf16 stores) and only one block's accumulators is
 // in VGPRs at a time.  The LDS must no longer be in use by the main loop (it
 // ends with a barrier); regions are wave-private, so no barrier is needed.
-// With NPRE > 0, pre(m_local, n_local, q) is called for every row of a block
-// before any row of it is visited: it issues the NPRE 16-byte loads the visit
-// needs into q, so a block's loads are all in flight together instead of
-// being waited for row group by row group, and the next block's loads are
-// issued before this block's rows are visited.
-template <class C, int NACC, int NPRE, class PRE, class F>
+// With a prefetch type QT other than NoPre, pre(m_local, n_local, q) is called
+// for every row of a block before any row of it is visited: it issues the
+// loads the visit needs into q (a QT), so a block's loads are all in flight
+// together instead of being waited for row group by row group, and the next
+// block's loads are issued before this block's rows are visited.
+struct NoPre {};
+template <class C, int NACC, class QT, class PRE, class F>
 MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, PRE&& pre,
                                F&& f) {
   static_assert(C::WM % 16 == 0, "rows are visited 16 at a time");
   constexpr int P = 36;  // padded row pitch (floats)
-  constexpr int NQ = NPRE > 0 ? NPRE : 1;
+  constexpr bool HAS_PRE = !std::is_same<QT, NoPre>::value;
   constexpr int SR = epi_rows<C, NACC>();  // rows staged per pass
   constexpr int NSP = C::WM / SR;          // passes per 32-column block
   constexpr int RG = SR / 16;              // row groups of a pass
@@ -805,19 +843,19 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
   float* reg = lds + wave * NACC * SR * P;
   // the loads of pass b + 1 are issued before the rows of pass b are visited
   // (two register sets), so their latency overlaps one pass of work
-  u32x4 q[2][RG][NQ];
+  QT q[2][RG];
   auto prefetch = [&](int b, int set) {
     const int r0 = wm * C::WM + (b % NSP) * SR;
 #pragma unroll
     for (int g = 0; g < RG; ++g)
       pre(r0 + g * 16 + (lane >> 2), wn * C::WN + (b / NSP) * 32 + (lane & 3) * 8, q[set][g]);
   };
-  if constexpr (NPRE > 0) prefetch(0, 0);
+  if constexpr (HAS_PRE) prefetch(0, 0);
 #pragma unroll
   for (int b = 0; b < NPASS; ++b) {  // unrolled: acc is indexed by constants only
     const int tn = b / NSP, sp = b % NSP, set = b & 1;
     const int r0 = wm * C::WM + sp * SR;  // first row of this pass
-    if constexpr (NPRE > 0) {
+    if constexpr (HAS_PRE) {
       if (b + 1 < NPASS) prefetch(b + 1, set ^ 1);
     }
 #pragma unroll
@@ -847,7 +885,7 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
       }
       f(r0 + row, wn * C::WN + tn * 32 + col, v, q[set][g]);
     };
-    if constexpr (NPRE > 0) {
+    if constexpr (HAS_PRE) {
 #pragma unroll
       for (int g = 0; g < RG; ++g) visit(g);  // q[set][g] needs constant indices
     } else {
@@ -860,20 +898,19 @@ MOE_DEV void for_each_row8_pre(const f32x16 (&acc)[NACC][C::TN][C::TM], float* l
 
 template <class C, int NACC, class F>
 MOE_DEV void for_each_row8(const f32x16 (&acc)[NACC][C::TN][C::TM], float* lds, F&& f) {
-  for_each_row8_pre<C, NACC, 0>(acc, lds, [](int, int, u32x4*) {},
-                                [&](int m, int n, auto& v, const u32x4*) { f(m, n, v); });
+  for_each_row8_pre<C, NACC, NoPre>(acc, lds, [](int, int, NoPre&) {},
+                                    [&](int m, int n, auto& v, const NoPre&) { f(m, n, v); });
 }
 
 // for_each_row8_pre over a tile that may be tall: the main blocks, then the
 // wave's extra blocks (C::XR > 0: rows BM + 32 (wm & 1) .., columns of half
 // wm >> 1 of its WN), staged the same way, 32 rows at a time.
-template <class C, int NACC, int NPRE, class PRE, class F>
+template <class C, int NACC, class QT, class PRE, class F>
 MOE_DEV void for_each_row8_xpre(const f32x16 (&acc)[NACC][C::TN][C::TM],
                                 const f32x16 (&xacc)[NACC][C::XTN], float* lds, PRE&& pre,
                                 F&& f) {
   auto extra = [&]() {
     constexpr int P = 36;
-    constexpr int NQ = NPRE > 0 ? NPRE : 1;
     constexpr int SR = epi_rows<C, NACC>();
     static_assert(SR >= 32, "one 32-row block per pass");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -883,8 +920,8 @@ MOE_DEV void for_each_row8_xpre(const f32x16 (&acc)[NACC][C::TN][C::TM],
     const int c0 = wn * C::WN + (C::XR == 128 ? 0 : (wm >> 1) * (C::WN / 2));
 #pragma unroll
     for (int j = 0; j < C::XTN; ++j) {
-      u32x4 q[2][NQ];
-      if constexpr (NPRE > 0) {
+      QT q[2];
+      if constexpr (!std::is_same<QT, NoPre>::value) {
 #pragma unroll
         for (int g = 0; g < 2; ++g) pre(r0 + g * 16 + (lane >> 2), c0 + j * 32 + (lane & 3) * 8, q[g]);
       }
@@ -920,17 +957,17 @@ MOE_DEV void for_each_row8_xpre(const f32x16 (&acc)[NACC][C::TN][C::TM],
     // the extra blocks first: their 64 accumulators are then dead during the
     // main passes (config 3 gate/up input gradient 1.20 -> 1.19 ms)
     extra();
-    for_each_row8_pre<C, NACC, NPRE>(acc, lds, pre, f);
+    for_each_row8_pre<C, NACC, QT>(acc, lds, pre, f);
   } else {
-    for_each_row8_pre<C, NACC, NPRE>(acc, lds, pre, f);
+    for_each_row8_pre<C, NACC, QT>(acc, lds, pre, f);
     if constexpr (C::XR > 0) extra();
   }
 }
 template <class C, int NACC, class F>
 MOE_DEV void for_each_row8_x(const f32x16 (&acc)[NACC][C::TN][C::TM],
                              const f32x16 (&xacc)[NACC][C::XTN], float* lds, F&& f) {
-  for_each_row8_xpre<C, NACC, 0>(acc, xacc, lds, [](int, int, u32x4*) {},
-                                 [&](int m, int n, auto& v, const u32x4*) { f(m, n, v); });
+  for_each_row8_xpre<C, NACC, NoPre>(acc, xacc, lds, [](int, int, NoPre&) {},
+                                     [&](int m, int n, auto& v, const NoPre&) { f(m, n, v); });
 }
 
 // Row epilogue for bf16 outputs that need no element-wise work beyond a scale:

@@ -1051,7 +1051,8 @@ __global__ __launch_bounds__(1024) void k_dispatch_small(const int* __restrict__
 template <typename T>
 __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
                                                 const int* __restrict__ inv_perm, int Tn, int k,
-                                                int H, T* __restrict__ xp) {
+                                                int H, T* __restrict__ xp,
+                                                const float* __restrict__ w = nullptr) {
   constexpr int V = Vec16<T>::N;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
@@ -1069,9 +1070,22 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
       const int pos = inv_perm[(int64_t)t * k + j];
       if (pos < 0 || pos >= TK) continue;
       T* dst = xp + (int64_t)pos * H;
+      if (w) {
+        const float wj = w[(int64_t)t * k + j];
 #pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (c0 + 64 * u < nv) st16(dst + (c0 + 64 * u) * V, buf[u]);
+        for (int u = 0; u < U; ++u)
+          if (c0 + 64 * u < nv) {
+            float f[V];
+            unpack16(buf[u], f, T());
+#pragma unroll
+            for (int i = 0; i < V; ++i) f[i] *= wj;
+            st16(dst + (c0 + 64 * u) * V, pack16(f, T()));
+          }
+      } else {
+#pragma unroll
+        for (int u = 0; u < U; ++u)
+          if (c0 + 64 * u < nv) st16(dst + (c0 + 64 * u) * V, buf[u]);
+      }
     }
   }
 }
@@ -1084,8 +1098,8 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
 // one ballot per choice; a token picks distinct experts, so each earlier
 // token counts at most once): expert ascending, then token ascending.  Lane j < k
 // writes perm and inv_perm for choice j; the row then goes to the k slots as
-// in k_gather.  A position outside [0, T k) (which valid routing never makes)
-// is skipped.
+// in k_gather (xp == nullptr: the scatter alone, no row is read or written).
+// A position outside [0, T k) (which valid routing never makes) is skipped.
 template <typename T>
 __global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ x,
                                                           const int* __restrict__ idx, int Tn,
@@ -1103,9 +1117,11 @@ __global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ 
   constexpr int U = 8;
   const int nv = H / V;
   u32x4 buf[U];
+  if (xp) {
 #pragma unroll
-  for (int u = 0; u < U; ++u)
-    if (lane + 64 * u < nv) buf[u] = ld16(src + (lane + 64 * u) * V);
+    for (int u = 0; u < U; ++u)
+      if (lane + 64 * u < nv) buf[u] = ld16(src + (lane + 64 * u) * V);
+  }
   const int grp = t >> 4, t0 = grp << 4;
   const int mine = lane < k ? idx[(int64_t)t * k + lane] : -1;
   const int* prev = idx + (int64_t)t0 * k;
@@ -1128,6 +1144,7 @@ __global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ 
       inv_perm[(int64_t)t * k + lane] = q;
     }
   }
+  if (!xp) return;
   // b0 is wave-uniform, so the loop and its broadcasts are too
   for (int b0 = 0;;) {
     const int c0 = b0 + lane;
@@ -1322,7 +1339,8 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_fwd(const T* __restrict__
                                                     const T* const* wg_tab, const T* wg_one,
                                                     const T* const* wu_tab, const T* wu_one,
                                                     int H, int N, T* __restrict__ G,
-                                                    T* __restrict__ U, T* __restrict__ A) {
+                                                    T* __restrict__ U, T* __restrict__ A,
+                                                    const int* __restrict__ perm, int Tn, int k) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 2, 2>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::AR, C::BN, grp, row0, mv, n0)) return;
@@ -1330,11 +1348,14 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_fwd(const T* __restrict__
   const T* wu = pick(wu_tab, wu_one, grp);
   with_tile_rows<T, C, 2>(mv, [&](auto ct) {
     using CT = decltype(ct);
+    // grouped: the token rows of x, gathered in expert order (row r is token
+    // perm[r] / k); dense: X's rows
     OpDesc<T> a[1] = {{X + (int64_t)row0 * H, H, mv, H}};
+    if constexpr (GROUPED) a[0] = {X, H, mv, H, perm + row0, Tn, k};
     OpDesc<T> b[2] = {{wg + (int64_t)n0 * H, H, N - n0, H}, {wu + (int64_t)n0 * H, H, N - n0, H}};
     f32x16 acc[2][CT::TN][CT::TM], xacc[2][CT::XTN];
     zero_acc<CT, 2>(acc, xacc);
-    mainloop_x<CT, T, false, false, 1, 2>(acc, xacc, a, b, H, smem);
+    mainloop_x<CT, T, false, false, 1, 2, GROUPED>(acc, xacc, a, b, H, smem);
     static_assert(epi_lds_floats<CT, 2>() * 4 <= (int)sizeof(smem), "epilogue LDS");
     for_each_row8_x<CT, 2>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
       if (m >= mv || n0 + n >= N) return;
@@ -1435,58 +1456,86 @@ __global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
   st16(out + (int64_t)t * H + c * V, pack16(acc, T()));
 }
 
-// dw[t, j] = <dout[t], Y[pos]>,  dY[pos] = w[t, j] * dout[t].
+// dY[pos] = w[t, j] * dout[t] for the down projection's weight gradient (its
+// input gradient reads d_out rows directly, and the combine weights' gradient
+// comes from that kernel's epilogue).  One wave per token: it reads the row
+// once, 8 vectors per lane at a time, and writes its k weighted copies.
 template <typename T>
 __global__ __launch_bounds__(256) void k_combine_bwd(const T* __restrict__ dout,
-                                                     const T* __restrict__ Y,
                                                      const int* __restrict__ inv_perm,
                                                      const float* __restrict__ w, int Tn, int k,
-                                                     int H, float* __restrict__ dw,
-                                                     T* __restrict__ dY) {
+                                                     int H, T* __restrict__ dY) {
   constexpr int V = Vec16<T>::N;
+  constexpr int U = 8;
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
   const int lane = threadIdx.x & 63;
   const int64_t TK = (int64_t)Tn * k;
-  int64_t pos[16];
-  float wj[16], dot[16];
-  for (int j = 0; j < k; ++j) {
-    int64_t p = inv_perm[(int64_t)t * k + j];
-    pos[j] = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
-    wj[j] = w[(int64_t)t * k + j];
-    dot[j] = 0.0f;
+  // lane j < k holds slot j's row and weight; read back wave-uniformly
+  int64_t mypos = 0;
+  float myw = 0.0f;
+  if (lane < k) {
+    const int64_t p = inv_perm[(int64_t)t * k + lane];
+    mypos = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+    myw = w[(int64_t)t * k + lane];
   }
-  for (int c = lane; c < H / V; c += 64) {
-    float d[V], y[V], o[V];
-    unpack16(ld16(dout + (int64_t)t * H + c * V), d, T());
-    for (int j = 0; j < k; ++j) {
-      unpack16(ld16(Y + pos[j] * H + c * V), y, T());
-      float s = 0.0f;
+  const int nv = H / V;
+  const T* src = dout + (int64_t)t * H;
+  for (int b0 = 0; b0 < nv; b0 += 64 * U) {
+    float d[U][V];
 #pragma unroll
-      for (int i = 0; i < V; ++i) {
-        s += d[i] * y[i];
-        o[i] = wj[j] * d[i];
+    for (int u = 0; u < U; ++u)
+      if (b0 + lane + 64 * u < nv) unpack16(ld16(src + (b0 + lane + 64 * u) * V), d[u], T());
+    for (int j = 0; j < k; ++j) {
+      const int64_t pj = __shfl(mypos, j, 64);
+      const float wj = __shfl(myw, j, 64);
+      T* dst = dY + pj * H;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int c = b0 + lane + 64 * u;
+        if (c < nv) {
+          float o[V];
+#pragma unroll
+          for (int i = 0; i < V; ++i) o[i] = wj * d[u][i];
+          st16(dst + c * V, pack16(o, T()));
+        }
       }
-      dot[j] += s;
-      st16(dY + pos[j] * H + c * V, pack16(o, T()));
     }
   }
-  for (int j = 0; j < k; ++j) {
-    const float r = wave_sum(dot[j]);
-    if (lane == 0) dw[(int64_t)t * k + j] = r;
-  }
+}
+
+// v of lane l ^ X within each group of four lanes (DPP quad_perm, X = 1 or 2).
+template <int X>
+MOE_DEV float quad_xor(float v) {
+  constexpr int ctrl = X == 1 ? 0xB1 : 0x4E;  // quad_perm [1,0,3,2] / [2,3,0,1]
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), ctrl, 0xF, 0xF, false));
 }
 
 // ------------------------------------------------------------------ expert GEMMs (backward)
 // dA = alpha * dY Wd (NN, K = H), then the SwiGLU backward in the epilogue:
 // dG = dA * U * silu'(G), dU = dA * silu(G).
+// GROUPED (routed experts): the A operand is the token rows of d_out itself,
+// gathered in expert order (permuted row r is token perm[r] / k), and the
+// routing weight w_r is left out: dY[r] = w_r d_out[t_r], so dA = w_r dA_u with
+// dA_u = d_out[t_r] Wd, and the epilogue writes the unweighted dG_u, dU_u
+// (dG = w_r dG_u, dU = w_r dU_u).  The weight is applied where those are
+// consumed: the gate/up weight gradient multiplies by w_r X[r] (its token rows
+// are built weighted), and dx adds w_tj times each gathered row of the gate/up
+// input gradient.  The epilogue also forms the combine weights' gradient from
+// the unweighted product: dw_r = <d_out[t_r], Y[r]> = <dA_u[r], A[r]> with
+// A = silu(G) U rebuilt from the G and U it loads anyway; each 32-column
+// block's part (8 products per lane, in order, then the 4 lanes of the row
+// as (l0 + l1) + (l2 + l3)) goes to dwp[block][r], and k_dw_sum adds the
+// blocks in order.  Dense (shared expert): dY = dY_dense, weight alpha.
 template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(C::THREADS) void k_down_dgrad(const T* __restrict__ dY, RowGroups groups,
                                                     const T* const* wd_tab, const T* wd_one,
                                                     int H, int N, float alpha,
                                                     const T* __restrict__ G,
                                                     const T* __restrict__ U,
-                                                    T* __restrict__ dG, T* __restrict__ dU) {
+                                                    T* __restrict__ dG, T* __restrict__ dU,
+                                                    const int* __restrict__ perm, int Tn, int k,
+                                                    float* __restrict__ dwp) {
   __shared__ __align__(16) T smem[rowcol_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, N, C::AR, C::BN, grp, row0, mv, n0)) return;
@@ -1496,47 +1545,87 @@ __global__ __launch_bounds__(C::THREADS) void k_down_dgrad(const T* __restrict__
   // resources start at the tile's first row and cover its mv rows, so the
   // 32-bit offsets stay small whatever the number of routed rows.
   constexpr int NV = (int)sizeof(T) / 2;  // 16-byte vectors per 8 elements
+  struct Pre {
+    u32x4 gu[2 * NV];  // G, then U
+  };
   const int64_t tile_base = (int64_t)row0 * N;
   const rsrc_t rg = make_rsrc(G + tile_base, (uint32_t)((int64_t)mv * N * sizeof(T)));
   const rsrc_t ru = make_rsrc(U + tile_base, (uint32_t)((int64_t)mv * N * sizeof(T)));
-  auto pre = [&](int m, int n, u32x4 (&q)[2 * NV]) {
+  auto pre = [&](int m, int n, Pre& q) {
     const bool in = m < mv && n0 + n < N;
     const uint32_t off = in ? (uint32_t)(((int64_t)m * N + n0 + n) * sizeof(T)) : kOobOffset;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
-      q[j] = buf_ld16(rg, off + 16 * j, 0);
-      q[NV + j] = buf_ld16(ru, off + 16 * j, 0);
+      q.gu[j] = buf_ld16(rg, off + 16 * j, 0);
+      q.gu[NV + j] = buf_ld16(ru, off + 16 * j, 0);
     }
   };
   with_tile_shape<T, C>(mv, N - n0, [&](auto ct) {
     using CT = decltype(ct);
     OpDesc<T> a[1] = {{dY + (int64_t)row0 * H, H, mv, H}};
+    if constexpr (GROUPED) a[0] = {dY, H, mv, H, perm + row0, Tn, k};
     OpDesc<T> b[1] = {{wd + n0, N, N - n0, H}};
     f32x16 acc[1][CT::TN][CT::TM], xacc[1][CT::XTN];
     zero_acc<CT, 1>(acc, xacc);
-    mainloop_x<CT, T, false, true, 1, 1>(acc, xacc, a, b, H, smem);
+    mainloop_x<CT, T, false, true, 1, 1, GROUPED>(acc, xacc, a, b, H, smem);
     static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8_xpre<CT, 1, 2 * NV>(acc, xacc, reinterpret_cast<float*>(smem), pre,
-                                     [&](int m, int n, auto& v, const u32x4 (&q)[2 * NV]) {
-      if (m >= mv || n0 + n >= N) return;
-      const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
+    for_each_row8_xpre<CT, 1, Pre>(acc, xacc, reinterpret_cast<float*>(smem), pre,
+                                   [&](int m, int n, auto& v, const Pre& q) {
+      const bool ok = m < mv && n0 + n < N;
       float g[8], u[8], dg[8], du[8];
 #pragma unroll
       for (int j = 0; j < NV; ++j) {
-        unpack16(q[j], g + j * (8 / NV), T());
-        unpack16(q[NV + j], u + j * (8 / NV), T());
+        unpack16(q.gu[j], g + j * (8 / NV), T());
+        unpack16(q.gu[NV + j], u + j * (8 / NV), T());
       }
+      float part = 0.0f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const float da = alpha * v[0][i];
+        const float da = alpha * v[0][i];  // grouped: unweighted, d_out Wd
         const float sg = sigmoid_f(g[i]);
+        const float gs = g[i] * sg;
+        if constexpr (GROUPED) part += ok ? da * (gs * u[i]) : 0.0f;
         dg[i] = da * u[i] * (sg * (1.0f + g[i] * (1.0f - sg)));
-        du[i] = da * (g[i] * sg);
+        du[i] = da * gs;
       }
+      if constexpr (GROUPED) {
+        // the row's 4 lanes (lane / 4 equal) hold its 32-column block; DPP
+        // quad permutes (lanes xor 1, then xor 2) keep the sum off the LDS
+        const float p1 = part + quad_xor<1>(part);
+        const float p2 = quad_xor<2>(p1);
+        const bool lo = (threadIdx.x & 2) == 0;
+        const float blk = lo ? p1 + p2 : p2 + p1;
+        if (m < mv && (threadIdx.x & 3) == 0 && n0 + n < N)
+          dwp[(int64_t)((n0 + n) >> 5) * groups.M + row0 + m] = blk;
+      }
+      if (!ok) return;
+      const int64_t o = (int64_t)(row0 + m) * N + n0 + n;
       store8(dG + o, dg);
       store8(dU + o, du);
     });
   });
+}
+
+// dw[perm[r]] = sum over the 32-column blocks c < nb of dwp[c][r] (c ascending):
+// the combine weights' gradient in (token, slot) order.
+__global__ __launch_bounds__(256) void k_dw_sum(const float* __restrict__ dwp, int nb, int TK,
+                                                const int* __restrict__ perm,
+                                                float* __restrict__ dw) {
+  const int r = blockIdx.x * 256 + threadIdx.x;
+  if (r >= TK) return;
+  // 16 loads in flight per thread, then added in block order
+  constexpr int U = 16;
+  float s = 0.0f;
+  for (int c0 = 0; c0 < nb; c0 += U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = c0 + u < nb ? dwp[(int64_t)(c0 + u) * TK + r] : 0.0f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (c0 + u < nb) s += v[u];
+  }
+  const int p = perm[r];
+  if ((unsigned)p < (unsigned)TK) dw[p] = s;
 }
 
 // dX = dG Wg + dU Wu (NN, K = I twice) per row group.
@@ -1756,7 +1845,9 @@ __global__ __launch_bounds__(256) void k_router_bwd(
   }
 }
 
-// dx = dlogits Wr (NN, K = E) + sum_j dXp[inv_perm[t, j]] + dxs[t].
+// dx = dlogits Wr (NN, K = E) + sum_j w[t, j] dXp[inv_perm[t, j]] + dxs[t]
+// (the rows of the gate/up input gradient are unweighted: w[t, j] multiplies
+// them here, one product per gathered element).
 // The whole fp32 accumulator tile is staged in LDS (rows of BN + 4 floats)
 // and read back by units of 8 outputs: 16 consecutive lanes cover 128
 // consecutive columns of one row, so every gathered dXp row segment is read
@@ -1764,7 +1855,7 @@ __global__ __launch_bounds__(256) void k_router_bwd(
 // at a time read half lines, whose other half came back from memory a block
 // later.)  KMAX >= k, a power of two, sizes the units each thread keeps in
 // flight.  Per output: the
-// accumulator, then the k gathered rows in slot order, then dxs.
+// accumulator, then the k weighted gathered rows in slot order, then dxs.
 template <typename T>
 constexpr int dgrad_smem_elems() {
   using C = typename Tilings<T>::RouterDx;
@@ -1777,6 +1868,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
                                                       const T* __restrict__ wr, int Tn, int H,
                                                       const T* __restrict__ dXp,
                                                       const int* __restrict__ inv_perm, int k,
+                                                      const float* __restrict__ topw,
                                                       const T* __restrict__ dxs,
                                                       T* __restrict__ dx) {
   using C = typename Tilings<T>::RouterDx;
@@ -1826,6 +1918,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
   static_assert(U >= 1 && (C::BM / 16) % U == 0, "units per step");
   for (int r0 = threadIdx.x >> 4; r0 < C::BM; r0 += 16 * U) {
     u32x4 raw[U][KMAX][NV], rs[U][NV];
+    float wt[U][KMAX];
     bool ok[U];
 #pragma unroll
     for (int h2 = 0; h2 < U; ++h2) {
@@ -1837,6 +1930,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
         if (j < k && ok[h2]) {
           int64_t p = inv_perm[(int64_t)t * k + j];
           p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
+          wt[h2][j] = topw[(int64_t)t * k + j];
 #pragma unroll
           for (int h = 0; h < NV; ++h)
             raw[h2][j][h] = *gptr(reinterpret_cast<const u32x4*>(dXp + p * H + n + h * (8 / NV)));
@@ -1863,7 +1957,7 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
 #pragma unroll
           for (int h = 0; h < NV; ++h) unpack16(raw[h2][j][h], q + h * (8 / NV), T());
 #pragma unroll
-          for (int i = 0; i < 8; ++i) v[i] += q[i];
+          for (int i = 0; i < 8; ++i) v[i] += wt[h2][j] * q[i];
         }
       }
       if (dxs) {

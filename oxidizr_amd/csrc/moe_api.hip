@@ -79,7 +79,7 @@ struct WsLayout {
   // forward
   size_t block_hist, block_base, colpart, ghist, gbase, gpart, rpart, sY, infer;
   // backward
-  size_t dw, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
+  size_t dw, dwp, dY, dG, dU, dXp, dlogits, dlogits_t, sdG, sdU, dxs, splitk_router, splitk_shared,
       recomp, dxm, dwn, dwn_a, dwn_b, xorder;
   size_t total;
   size_t fwd_total;  // bytes a forward-only call touches (the forward regions)
@@ -311,11 +311,14 @@ struct moe_plan {
     fld(MOE_SAVED_MEAN_PROB, 4 * (size_t)E);
     L.tile_prefix = c.take(4 * (size_t)kTilePrefixes * kNumTileBM * (E + 1));
     const bool act = keep != Keep::Routing, pre = keep == Keep::All;
-    fld(MOE_SAVED_X_PERM, act ? b * TK * H : 0);
+    // the GEMMs read x through the permutation: no permuted copy is kept
+    fld(MOE_SAVED_X_PERM, 0);
     fld(MOE_SAVED_GATE_ACT, pre ? b * TK * I : 0);
     fld(MOE_SAVED_UP_ACT, pre ? b * TK * I : 0);
     fld(MOE_SAVED_SWIGLU, act ? b * TK * I : 0);
-    fld(MOE_SAVED_EXPERT_OUT, act ? b * TK * H : 0);
+    // the expert outputs feed the forward's combine only (the backward forms
+    // the combine weights' gradient from d_out Wd and A): transient state
+    fld(MOE_SAVED_EXPERT_OUT, keep == Keep::Transient ? b * TK * H : 0);
     const bool blk = cfg.fused_block != 0 && act;
     fld(MOE_SAVED_RSTD, blk ? 4 * (size_t)T : 0);
     fld(MOE_SAVED_NORM_X, blk ? b * T * H : 0);
@@ -365,6 +368,11 @@ struct moe_plan {
     // column partials of the router-bias gradient (offset 0)
     put(g, "bias_colpart", 4 * (size_t)nrb * E);
     L.dw = put(g, "dw", 4 * TK);
+    // the combine weights' gradient per 32-column block of the down
+    // projection's input gradient
+    L.dwp = put(g, "dwp", 4 * (size_t)ceil_div(I, 32) * TK);
+    // the weighted d_out rows of the down projection's weight gradient, then
+    // (same stream, after it) the weighted token rows of the gate/up one
     L.dY = put(g, "dY", b * TK * H);
     L.dG = put(g, "dG", b * TK * I);
     L.dU = put(g, "dU", b * TK * I);
@@ -758,7 +766,7 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
       using C = decltype(c);
       hipLaunchKernelGGL((k_gateup_fwd<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, x, dense,
                          nullptr, (const D*)w->shared_gate, nullptr, (const D*)w->shared_up, H, S,
-                         sG, sU, sA);
+                         sG, sU, sA, nullptr, 0, 1);
     });
     if (sY)
       with_dense_tiling<D, CB>(T, H, [&](auto c, int grid) {
@@ -815,11 +823,13 @@ void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t 
     [mt](int N) { return 8 * ceil_div(mt * ceil_div(N, C::BN), 8); });
 }
 
-// Routed experts forward on stream s: gather X_perm, then G, U (when kept),
-// A and the per-assignment expert outputs Y.  `timed`: record the stages.
+// Routed experts forward on stream s: G, U (when kept), A and the
+// per-assignment expert outputs Y (when st.Y is set: a recomputing backward
+// needs none).  The GEMMs read each assignment's token row of x through the
+// permutation (no permuted copy of x).  `timed`: record the stages.
 // `gbase` (not null): the dispatch stopped after k_scan over the fused
-// router's 16-token groups, whose bases gbase holds, and the gather also
-// writes perm and inv_perm.
+// router's 16-token groups, whose bases gbase holds; k_scatter_gather16
+// then writes perm and inv_perm.
 template <typename D>
 moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State<D>& st,
                       bool timed, const int* gbase = nullptr) {
@@ -831,24 +841,14 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   auto stage = [&](int id) { return timed ? id : MOE_STAGE_RECOMPUTE; };
   // few tokens: no expert holds more than T rows, stream the weights instead
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
-  // X_perm is read by the tiled GEMMs and, when the gate / up pre-activations
-  // are kept (a backward follows and reads saved state), by the weight
-  // gradient; otherwise the small-token kernel reads each assignment's token
-  // row of x directly.
-  const bool gather = !skinny || st.G != nullptr;
-  if (gbase && !gather) return fail(MOE_ERR_INVALID, "deferred scatter without a gather");
-  if (gather) {
+  if (gbase) {
     StageTimer tm(p, s, stage(MOE_STAGE_GATHER));
-    if (gbase)
-      hipLaunchKernelGGL(k_scatter_gather16<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.idx,
-                         T, k, E, H, gbase, st.perm, st.inv, st.xp);
-    else
-      hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.inv, T, k, H,
-                         st.xp);
+    hipLaunchKernelGGL(k_scatter_gather16<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.idx,
+                       T, k, E, H, gbase, st.perm, st.inv, (D*)nullptr);
     LAUNCH_CHECK();
   }
-  const bf16_t* xsrc = (const bf16_t*)(gather ? st.xp : x);
-  const int* xrow = gather ? nullptr : st.perm;
+  const bf16_t* xsrc = (const bf16_t*)x;
+  const int* xrow = st.perm;
   const D* const* tg = (const D* const*)p->d_tab;
   const D* const* tu = (const D* const*)(p->d_tab + E);
   const D* const* td = (const D* const*)(p->d_tab + 2 * E);
@@ -868,11 +868,13 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
       with_row_tiling<D, CG>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
         using C = decltype(c);
         hipLaunchKernelGGL((k_gateup_fwd<D, true, C>), dim3(grid(I)), dim3(C::THREADS), 0,
-                           s, st.xp, r, tg, nullptr, tu, nullptr, H, I, st.G, st.U, st.A);
+                           s, x, r, tg, nullptr, tu, nullptr, H, I, st.G, st.U, st.A, st.perm,
+                           T, k);
       });
     }
     LAUNCH_CHECK();
   }
+  if (!st.Y) return MOE_OK;  // a recomputing backward needs no expert outputs
   {
     StageTimer tm(p, s, stage(MOE_STAGE_DOWN_FWD));
     if (skinny) {
@@ -918,7 +920,10 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   const SavedLayout LR = train ? p->kept_layout(T64) : LT;
   char* rb = train ? saved : ws + W.infer;
   char* ab = keep_act ? saved : ws + W.infer;
-  const State<D> st(rb, LR, ab, keep_act ? LR : LT);
+  State<D> st(rb, LR, ab, keep_act ? LR : LT);
+  // a kept training forward still needs the expert outputs for its combine:
+  // they go to the forward-only region, unused by such a call
+  if (!st.Y) st.Y = (D*)(ws + W.infer + LT.f[MOE_SAVED_EXPERT_OUT]);
   // Shared expert first, on the plan's second stream: it only needs x.
   D* sY = nullptr;
   SideJoin shared_join, p_join;
@@ -1068,11 +1073,9 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   const float* probs = st.probs;
   const float* lse = st.lse;
   const float* P = st.P;
-  const D* xp = st.xp;
   const D* G = st.G;
   const D* U = st.U;
   const D* A = st.A;
-  const D* Y = st.Y;
   float* dw = (float*)(ws + W.dw);
   D* dY = (D*)(ws + W.dY);
   D* dG = (D*)(ws + W.dG);
@@ -1116,7 +1119,8 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     with_dense_tiling<D, CB>(T, S, [&](auto c, int grid) {
       using C = decltype(c);
       hipLaunchKernelGGL((k_down_dgrad<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, dout,
-                         dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU, sdG, sdU);
+                         dense, nullptr, (const D*)w->shared_down, H, S, sc, sG, sU, sdG, sdU,
+                         nullptr, 0, 1, nullptr);
     });
     with_dense_tiling<D, CB>(T, H, [&](auto c, int grid) {
       using C = decltype(c);
@@ -1140,17 +1144,20 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     moe_status r = routed_fwd<D>(p, s, T, x, st, false);
     if (r != MOE_OK) return r;
   }
-  {
-    StageTimer tm(p, s, MOE_STAGE_COMBINE_BWD);
-    hipLaunchKernelGGL(k_combine_bwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, dout, Y, inv,
-                       topw, T, k, H, dw, dY);
-    LAUNCH_CHECK();
-  }
+  float* dwp = (float*)(ws + W.dwp);
   // From here the routed weight gradients run on the weight-gradient stream
   // ws2 (they read dY, A, X_perm and, after the down projection's input
   // gradient, dG / dU); the input gradients and the router backward on s.
   const hipStream_t ws2 = p->wgrad_stream(s);
   HIP_TRY(wgrad_join.fork(s, ws2, p->wfork, p->wjoin));
+  {
+    // the weighted copies of d_out only the down projection's weight
+    // gradient reads: beside the input gradient on s
+    StageTimer tm(p, ws2, MOE_STAGE_COMBINE_BWD);
+    hipLaunchKernelGGL(k_combine_bwd<D>, dim3(ceil_div(T, 4)), dim3(256), 0, ws2, dout, inv,
+                       topw, T, k, H, dY);
+    LAUNCH_CHECK();
+  }
   // whole experts per XCD for the gate/up weight gradient when the experts
   // split evenly over the XCDs (k_xcd_order decides on the device)
   int* xorder = E % 8 == 0 ? (int*)(ws + W.xorder) : nullptr;
@@ -1185,8 +1192,23 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     with_row_tiling<D, CB, false>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
       hipLaunchKernelGGL((k_down_dgrad<D, true, C>), dim3(grid(I)), dim3(C::THREADS), 0, s,
-                         dY, r, td, nullptr, H, I, 1.0f, G, U, dG, dU);
+                         dout, r, td, nullptr, H, I, 1.0f, G, U, dG, dU, st.perm, T, k, dwp);
     });
+    LAUNCH_CHECK();
+    hipLaunchKernelGGL(k_dw_sum, dim3(ceil_div(TK, (int64_t)256)), dim3(256), 0, s, dwp,
+                       ceil_div(I, 32), (int)TK, st.perm, dw);
+    LAUNCH_CHECK();
+  }
+  // the gate/up weight gradient's token rows, weighted (its dG_u, dU_u leave
+  // the routing weight out), in dY's region once the down projection's
+  // weight gradient has read it (same stream).  Launched after the input
+  // gradient on s, so a serial run (one stream) keeps the order of the
+  // overlapped one for the caches: d_out rows, G and U are read first.
+  D* xw = dY;
+  {
+    StageTimer tm(p, ws2, MOE_STAGE_GATHER);
+    hipLaunchKernelGGL(k_gather<D>, dim3(ceil_div(T, 4)), dim3(256), 0, ws2, x, inv, T, k, H, xw,
+                       topw);
     LAUNCH_CHECK();
   }
   if (ws2 != s) {
@@ -1199,7 +1221,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     KGroups kgp = kg;
     kgp.xcd_order = xorder;
     const int slots = std::min(grid, p->wgrad_slots);
-    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(expect_whole ? slots : grid), dim3(CW::THREADS), 0, ws2, dG, dU, (int64_t)I, xp,
+    hipLaunchKernelGGL((k_wgrad<D, 2, true>), dim3(expect_whole ? slots : grid), dim3(CW::THREADS), 0, ws2, dG, dU, (int64_t)I, xw,
                        (int64_t)H, kgp, I, H, 1.0f, tdg, nullptr, tdu, nullptr, nullptr, grid,
                        slots);
     LAUNCH_CHECK();
@@ -1247,13 +1269,13 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     const dim3 grid(ceil_div(T, CX::BM) * ceil_div(H, CX::BN));
     const D* wr = (const D*)w->router;
     if (k <= 2)
-      hipLaunchKernelGGL((k_router_dgrad<D, 2>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 2>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
     else if (k <= 4)
-      hipLaunchKernelGGL((k_router_dgrad<D, 4>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 4>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
     else if (k <= 8)
-      hipLaunchKernelGGL((k_router_dgrad<D, 8>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 8>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
     else
-      hipLaunchKernelGGL((k_router_dgrad<D, 16>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 16>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
     if (has_grad) hipLaunchKernelGGL(k_has_grad, dim3(ceil_div(E, 256)), dim3(256), 0, s, counts, E, has_grad);
     LAUNCH_CHECK();
   }

@@ -508,9 +508,18 @@ def test_recompute_shrinks_saved_state():
     keep = Plan(MoeConfig(**kw), torch.bfloat16, dev)
     rec = Plan(MoeConfig(recompute_activations=True, **kw), torch.bfloat16, dev)
     T = 1000
-    # routing state only: no [T*k, H] / [T*k, I] / [T, S] activation is kept
-    act = 2 * (T * 2 * 256 * 2 + T * 2 * 128 * 3 + T * 128 * 3)
+    # routing state only: no [T*k, I] / [T, S] activation is kept (a kept
+    # forward holds G / U / A and the shared G / U / A; neither keeps a
+    # [T*k, H] row: the GEMMs read x through the permutation and the expert
+    # outputs Y are transient)
+    act = 2 * (T * 2 * 128 * 3 + T * 128 * 3)
     assert keep.saved_bytes(T) - rec.saved_bytes(T) >= act
+    for plan in (keep, rec):
+        for field in ("x_perm", "expert_out"):
+            off, nb = ctypes.c_size_t(), ctypes.c_size_t()
+            _lib.check(_lib.load().moe_saved_field_range(
+                plan.h, T, _lib.SAVED_FIELDS.index(field), ctypes.byref(off), ctypes.byref(nb)))
+            assert nb.value == 0, field
     assert rec.saved_bytes(T) < 40 * T * 16
     assert rec.workspace_bytes(T) > keep.workspace_bytes(T)
 
