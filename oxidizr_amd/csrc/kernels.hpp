@@ -1372,11 +1372,15 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_fwd(const T* __restrict__
   });
 }
 
-// Y = A Wd^T per row group (K = I) or for the dense shared expert.
+// Y = A Wd^T per row group (K = I) or for the dense shared expert.  orow
+// (grouped, not null): output row r goes to row orow[r] (the permutation:
+// slot t * k + j), so the combine reads a token's k rows as one contiguous
+// block; the row indices of a pass are loaded one pass ahead.
 template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(C::THREADS) void k_down_fwd(const T* __restrict__ A, RowGroups groups,
                                                   const T* const* wd_tab, const T* wd_one, int I,
-                                                  int H, T* __restrict__ Y) {
+                                                  int H, T* __restrict__ Y,
+                                                  const int* __restrict__ orow) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::AR, C::BN, grp, row0, mv, n0)) return;
@@ -1389,16 +1393,29 @@ __global__ __launch_bounds__(C::THREADS) void k_down_fwd(const T* __restrict__ A
     zero_acc<CT, 1>(acc, xacc);
     mainloop_x<CT, T, false, false, 1, 1>(acc, xacc, a, b, I, smem);
     static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8_x<CT, 1>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
-      if (m >= mv || n0 + n >= H) return;
-      store8(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
-    });
+    if (GROUPED && orow) {
+      struct Pre { int r; };
+      const rsrc_t ro = make_rsrc(orow + row0, (uint32_t)mv * 4u);
+      for_each_row8_xpre<CT, 1, Pre>(acc, xacc, reinterpret_cast<float*>(smem),
+                                     [&](int m, int, Pre& q) {
+        q.r = (int)__builtin_amdgcn_raw_buffer_load_b32(ro, m < mv ? (uint32_t)m * 4u : kOobOffset, 0, 0);
+      }, [&](int m, int n, auto& v, const Pre& q) {
+        if (m >= mv || n0 + n >= H) return;
+        store8(Y + (int64_t)q.r * H + n0 + n, v[0]);
+      });
+    } else {
+      for_each_row8_x<CT, 1>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+        if (m >= mv || n0 + n >= H) return;
+        store8(Y + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+      });
+    }
   });
 }
 
 // ------------------------------------------------------------------ combine
 // out[t] = sum_j w[t, j] * Y[inv_perm[t, j]] (+ s * Ys[t]) (+ resid[t]), added in
-// that order in fp32 and rounded once.  One wave per (token, slice of 64
+// that order in fp32 and rounded once (inv_perm == nullptr: Y is token-major,
+// row t * k + j, as the grouped down projection writes it).  One wave per (token, slice of 64
 // 16-byte vectors of the row); the k expert rows of a slice are all requested
 // before the first one is added.
 constexpr int kCombineSlice = 64;  // 16-byte vectors per wave
@@ -1423,7 +1440,7 @@ __global__ __launch_bounds__(256) void k_combine_fwd(const T* __restrict__ Y,
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     if (j < k) {
-      int64_t p = inv_perm[(int64_t)t * k + j];
+      int64_t p = inv_perm ? inv_perm[(int64_t)t * k + j] : (int64_t)t * k + j;
       p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
       wj[j] = w[(int64_t)t * k + j];
       ya[j] = ld16(Y + p * H + c * V);
@@ -1628,13 +1645,17 @@ __global__ __launch_bounds__(256) void k_dw_sum(const float* __restrict__ dwp, i
   if ((unsigned)p < (unsigned)TK) dw[p] = s;
 }
 
-// dX = dG Wg + dU Wu (NN, K = I twice) per row group.
+// dX = dG Wg + dU Wu (NN, K = I twice) per row group.  orow (grouped, not
+// null): output row r goes to row orow[r] (the permutation: slot t * k + j),
+// so dx reads a token's k rows as one contiguous block; the row indices of a
+// pass are loaded one pass ahead with the epilogue's prefetch.
 template <typename T, bool GROUPED, class C = typename Tilings<T>::Big>
 __global__ __launch_bounds__(C::THREADS) void k_gateup_dgrad(const T* __restrict__ dG,
                                                       const T* __restrict__ dU, RowGroups groups,
                                                       const T* const* wg_tab, const T* wg_one,
                                                       const T* const* wu_tab, const T* wu_one,
-                                                      int I, int H, T* __restrict__ dX) {
+                                                      int I, int H, T* __restrict__ dX,
+                                                      const int* __restrict__ orow) {
   __shared__ __align__(16) T smem[rowgroup_smem_elems<T, C, 1, 1, 1>()];
   int grp, row0, mv, n0;
   if (!resolve_rows(groups, H, C::AR, C::BN, grp, row0, mv, n0)) return;
@@ -1651,10 +1672,22 @@ __global__ __launch_bounds__(C::THREADS) void k_gateup_dgrad(const T* __restrict
     OpDesc<T> b2[1] = {{wu + n0, H, H - n0, I}};
     mainloop_x<CT, T, false, true, 1, 1>(acc, xacc, a, b, I, smem, a2, b2, I);
     static_assert(epi_lds_floats<CT, 1>() * 4 <= (int)sizeof(smem), "epilogue LDS");
-    for_each_row8_x<CT, 1>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
-      if (m >= mv || n0 + n >= H) return;
-      store8(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
-    });
+    if (GROUPED && orow) {
+      struct Pre { int r; };
+      const rsrc_t ro = make_rsrc(orow + row0, (uint32_t)mv * 4u);
+      for_each_row8_xpre<CT, 1, Pre>(acc, xacc, reinterpret_cast<float*>(smem),
+                                     [&](int m, int, Pre& q) {
+        q.r = (int)__builtin_amdgcn_raw_buffer_load_b32(ro, m < mv ? (uint32_t)m * 4u : kOobOffset, 0, 0);
+      }, [&](int m, int n, auto& v, const Pre& q) {
+        if (m >= mv || n0 + n >= H) return;
+        store8(dX + (int64_t)q.r * H + n0 + n, v[0]);
+      });
+    } else {
+      for_each_row8_x<CT, 1>(acc, xacc, reinterpret_cast<float*>(smem), [&](int m, int n, auto& v) {
+        if (m >= mv || n0 + n >= H) return;
+        store8(dX + (int64_t)(row0 + m) * H + n0 + n, v[0]);
+      });
+    }
   });
 }
 
@@ -1847,7 +1880,8 @@ __global__ __launch_bounds__(256) void k_router_bwd(
 
 // dx = dlogits Wr (NN, K = E) + sum_j w[t, j] dXp[inv_perm[t, j]] + dxs[t]
 // (the rows of the gate/up input gradient are unweighted: w[t, j] multiplies
-// them here, one product per gathered element).
+// them here, one product per gathered element).  inv_perm == nullptr: dXp is
+// token-major (row t * k + j), as the grouped gate/up input gradient writes it.
 // The whole fp32 accumulator tile is staged in LDS (rows of BN + 4 floats)
 // and read back by units of 8 outputs: 16 consecutive lanes cover 128
 // consecutive columns of one row, so every gathered dXp row segment is read
@@ -1928,7 +1962,8 @@ __global__ __launch_bounds__(256) void k_router_dgrad(const T* __restrict__ dl, 
 #pragma unroll
       for (int j = 0; j < KMAX; ++j) {
         if (j < k && ok[h2]) {
-          int64_t p = inv_perm[(int64_t)t * k + j];
+          // token-major rows (inv_perm null) or expert-major ones
+          int64_t p = inv_perm ? inv_perm[(int64_t)t * k + j] : (int64_t)t * k + j;
           p = p < 0 ? 0 : (p >= TK ? TK - 1 : p);
           wt[h2][j] = topw[(int64_t)t * k + j];
 #pragma unroll

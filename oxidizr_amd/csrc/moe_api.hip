@@ -772,7 +772,7 @@ void shared_fwd(moe_plan* p, hipStream_t ss, int T, const D* x, const moe_weight
       with_dense_tiling<D, CB>(T, H, [&](auto c, int grid) {
         using C = decltype(c);
         hipLaunchKernelGGL((k_down_fwd<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, sA, dense,
-                           nullptr, (const D*)w->shared_down, S, H, sY);
+                           nullptr, (const D*)w->shared_down, S, H, sY, nullptr);
       });
   }
 }
@@ -889,7 +889,7 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
       with_row_tiling<D, CB>(st.offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
         using C = decltype(c);
         hipLaunchKernelGGL((k_down_fwd<D, true, C>), dim3(grid(H)), dim3(C::THREADS), 0, s,
-                           st.A, r, td, nullptr, I, H, st.Y);
+                           st.A, r, td, nullptr, I, H, st.Y, st.perm);
       });
     }
     LAUNCH_CHECK();
@@ -998,10 +998,8 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     }
     LAUNCH_CHECK();
   }
-  // the fused router's scatter runs inside the gather: every fused call has
-  // T > kRouteSmallTokens = kSkinnyMaxTokens, so its routed forward gathers X_perm
-  static_assert(kSkinnyMaxTokens == kRouteSmallTokens,
-                "a fused-router batch is never a small-token batch: its gather writes perm");
+  // the fused router's dispatch stops after k_scan; the routed forward's
+  // first launch (k_scatter_gather16, scatter only) writes perm and inv_perm
   const bool defer = fused;
   moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused);
   if (r != MOE_OK) return r;
@@ -1022,8 +1020,11 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
   {
     StageTimer tm(p, s, MOE_STAGE_COMBINE_FWD);
     const int nsl = ceil_div(H / (16 / (int)sizeof(D)), kCombineSlice);
+    // the tiled down projection writes Y token-major; the small-token kernel
+    // in expert order
+    const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
     hipLaunchKernelGGL(k_combine_fwd<D>, dim3(ceil_div((int64_t)T * nsl, 4)), dim3(256), 0, s,
-                       st.Y, st.inv,
+                       st.Y, skinny ? st.inv : nullptr,
                        st.w, sY, c.shared_expert_scale, T, k, H, resid, out);
     LAUNCH_CHECK();
   }
@@ -1126,7 +1127,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
       using C = decltype(c);
       hipLaunchKernelGGL((k_gateup_dgrad<D, false, C>), dim3(grid), dim3(C::THREADS), 0, ss, sdG,
                          sdU, dense, nullptr, (const D*)w->shared_gate, nullptr,
-                         (const D*)w->shared_up, S, H, dxs);
+                         (const D*)w->shared_up, S, H, dxs, nullptr);
     });
     if (ss != s) {
       HIP_TRY(hipEventRecord(p->sdx, ss));
@@ -1231,7 +1232,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     with_row_tiling<D, CB>(offsets, st.tprefix, E, TK, [&](auto c, const RowGroups& r, auto grid) {
       using C = decltype(c);
       hipLaunchKernelGGL((k_gateup_dgrad<D, true, C>), dim3(grid(H)), dim3(C::THREADS), 0,
-                         s, dG, dU, r, tg, nullptr, tu, nullptr, I, H, dXp);
+                         s, dG, dU, r, tg, nullptr, tu, nullptr, I, H, dXp, st.perm);
     });
     LAUNCH_CHECK();
   }
@@ -1269,13 +1270,13 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
     const dim3 grid(ceil_div(T, CX::BM) * ceil_div(H, CX::BN));
     const D* wr = (const D*)w->router;
     if (k <= 2)
-      hipLaunchKernelGGL((k_router_dgrad<D, 2>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 2>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, nullptr, k, topw, dxs, dx);
     else if (k <= 4)
-      hipLaunchKernelGGL((k_router_dgrad<D, 4>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 4>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, nullptr, k, topw, dxs, dx);
     else if (k <= 8)
-      hipLaunchKernelGGL((k_router_dgrad<D, 8>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 8>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, nullptr, k, topw, dxs, dx);
     else
-      hipLaunchKernelGGL((k_router_dgrad<D, 16>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, inv, k, topw, dxs, dx);
+      hipLaunchKernelGGL((k_router_dgrad<D, 16>), grid, dim3(256), 0, s, dlt, Epad, E, wr, T, H, dXp, nullptr, k, topw, dxs, dx);
     if (has_grad) hipLaunchKernelGGL(k_has_grad, dim3(ceil_div(E, 256)), dim3(256), 0, s, counts, E, has_grad);
     LAUNCH_CHECK();
   }
