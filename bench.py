@@ -294,9 +294,11 @@ def measure(args, config, steps, warmup, extras=True):
     # (operands read once, outputs written once; weights of the experts that
     # received tokens).
     gemm_work = {
-        "gateup_fwd": (4 * TK * H * I, TK * H * b + 2 * n_touched * I * H * b + 3 * TK * I * b),
+        # the token operands of the gate/up forward and of the down input
+        # gradient are x and d_out read through the permutation: T rows
+        "gateup_fwd": (4 * TK * H * I, T * H * b + 2 * n_touched * I * H * b + 3 * TK * I * b),
         "down_fwd": (2 * TK * I * H, TK * I * b + n_touched * H * I * b + TK * H * b),
-        "down_dgrad": (2 * TK * H * I, TK * H * b + n_touched * H * I * b + 4 * TK * I * b),
+        "down_dgrad": (2 * TK * H * I, T * H * b + n_touched * H * I * b + 4 * TK * I * b),
         "gateup_dgrad": (4 * TK * I * H, 2 * TK * I * b + 2 * n_touched * I * H * b + TK * H * b),
         "down_wgrad": (2 * TK * H * I, TK * H * b + TK * I * b + n_touched * H * I * b),
         "gateup_wgrad": (4 * TK * H * I, 2 * TK * I * b + TK * H * b + 2 * n_touched * I * H * b),
