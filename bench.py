@@ -328,11 +328,13 @@ def measure(args, config, steps, warmup, extras=True):
         plan.set_profiling(list(gemm_work))
         for _ in range(3):
             step()
-        alone = {n: ms / c for n, (ms, c) in plan.stage_times(reset=True).items() if c}
+        # per step: a stage may be recorded more than once per step (the
+        # dispatch: k_scan and the scatter)
+        alone = {n: ms / 3 for n, (ms, c) in plan.stage_times(reset=True).items() if c}
         plan.set_shared_overlap(True)
         for _ in range(2):
             step()
-        insitu = {n: ms / c for n, (ms, c) in plan.stage_times(reset=True).items() if c}
+        insitu = {n: ms / 2 for n, (ms, c) in plan.stage_times(reset=True).items() if c}
         dominant = max((n for n in gemm_work if n in alone), key=lambda n: alone[n])
     else:  # forward-only small-token path: the gate/up weight stream
         dominant = "gateup_fwd"
@@ -354,7 +356,7 @@ def measure(args, config, steps, warmup, extras=True):
     plan.set_profiling(None)
     for _ in range(3):
         step()
-    stages = {n: ms / c for n, (ms, c) in plan.stage_times(reset=True).items() if c}
+    stages = {n: ms / 3 for n, (ms, c) in plan.stage_times(reset=True).items() if c}
     plan.set_profiling([])
     plan.set_shared_overlap(True)
 

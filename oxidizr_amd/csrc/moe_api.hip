@@ -841,8 +841,8 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   auto stage = [&](int id) { return timed ? id : MOE_STAGE_RECOMPUTE; };
   // few tokens: no expert holds more than T rows, stream the weights instead
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
-  if (gbase) {
-    StageTimer tm(p, s, stage(MOE_STAGE_GATHER));
+  if (gbase) {  // the dispatch's last launch
+    StageTimer tm(p, s, stage(MOE_STAGE_DISPATCH));
     hipLaunchKernelGGL(k_scatter_gather16<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.idx,
                        T, k, E, H, gbase, st.perm, st.inv, (D*)nullptr);
     LAUNCH_CHECK();
