@@ -1421,6 +1421,7 @@ moe_status check_workspace_plan(const moe_plan& p, int64_t T) {
     add("infer", p.saved_layout(T, moe_plan::Keep::Transient).total);
     if (c.has_router_bias) add("bias_colpart", 4 * (size_t)colsum_rows(T, false) * E);
     add("dw", 4 * TK);
+    add("dwp", 4 * (size_t)ceil_div(I, 32) * TK);
     add("dY", b * TK * H);
     add("dG", b * TK * I);
     add("dU", b * TK * I);
