@@ -174,6 +174,8 @@ class Plan:
         off, nb = ctypes.c_size_t(), ctypes.c_size_t()
         _lib.check(_lib.load().moe_saved_field_range(self.h, T, f, ctypes.byref(off),
                                                      ctypes.byref(nb)))
+        if nb.value == 0:
+            raise ValueError(f"saved field {name!r} is not kept by this plan (0 bytes)")
         raw = saved[off.value:off.value + nb.value]
         E, k, H, I = self.c.num_experts, self.c.experts_per_tok, self.c.hidden, self.c.intermediate
         shapes = {
