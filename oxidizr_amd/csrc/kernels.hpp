@@ -1090,38 +1090,25 @@ __global__ __launch_bounds__(256) void k_gather(const T* __restrict__ x,
   }
 }
 
-// The stable scatter and k_gather in one launch (after the fused router and
-// k_scan over its 16-token groups).  The wave of token t first issues its row's
-// loads, then finds where each of its k choices goes: the base of its group
-// and expert plus the number of earlier tokens of the group that chose the
-// same expert, counted from the group's idx entries before t's (64 at a time,
-// one ballot per choice; a token picks distinct experts, so each earlier
-// token counts at most once): expert ascending, then token ascending.  Lane j < k
-// writes perm and inv_perm for choice j; the row then goes to the k slots as
-// in k_gather (xp == nullptr: the scatter alone, no row is read or written).
-// A position outside [0, T k) (which valid routing never makes) is skipped.
-template <typename T>
-__global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ x,
-                                                          const int* __restrict__ idx, int Tn,
-                                                          int k, int E, int H,
-                                                          const int* __restrict__ group_base,
-                                                          int* __restrict__ perm,
-                                                          int* __restrict__ inv_perm,
-                                                          T* __restrict__ xp) {
-  constexpr int V = Vec16<T>::N;
+// The stable scatter of the fused router's 16-token groups (after the fused
+// router and k_scan over its groups).  The wave of token t finds where each
+// of its k choices goes: the base of its group and expert plus the number of
+// earlier tokens of the group that chose the same expert, counted from the
+// group's idx entries before t's (64 at a time, one ballot per choice; a
+// token picks distinct experts, so each earlier token counts at most once):
+// expert ascending, then token ascending.  Lane j < k writes perm and
+// inv_perm for choice j.  A position outside [0, T k) (which valid routing
+// never makes) is skipped.  No row is copied: the expert GEMMs read token
+// rows through perm.
+__global__ __launch_bounds__(256) void k_scatter_groups(const int* __restrict__ idx, int Tn,
+                                                        int k, int E,
+                                                        const int* __restrict__ group_base,
+                                                        int* __restrict__ perm,
+                                                        int* __restrict__ inv_perm) {
   const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (t >= Tn) return;
   const int lane = threadIdx.x & 63;
   const int64_t TK = (int64_t)Tn * k;
-  const T* src = x + (int64_t)t * H;
-  constexpr int U = 8;
-  const int nv = H / V;
-  u32x4 buf[U];
-  if (xp) {
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (lane + 64 * u < nv) buf[u] = ld16(src + (lane + 64 * u) * V);
-  }
   const int grp = t >> 4, t0 = grp << 4;
   const int mine = lane < k ? idx[(int64_t)t * k + lane] : -1;
   const int* prev = idx + (int64_t)t0 * k;
@@ -1135,32 +1122,12 @@ __global__ __launch_bounds__(256) void k_scatter_gather16(const T* __restrict__ 
       if (lane == j) rank += n;
     }
   }
-  int pos = -1;
   if (lane < k && mine >= 0 && mine < E) {
     const int q = group_base[(int64_t)grp * E + mine] + rank;
     if (q >= 0 && q < TK) {
-      pos = q;
       perm[q] = t * k + lane;
       inv_perm[(int64_t)t * k + lane] = q;
     }
-  }
-  if (!xp) return;
-  // b0 is wave-uniform, so the loop and its broadcasts are too
-  for (int b0 = 0;;) {
-    const int c0 = b0 + lane;
-    for (int j = 0; j < k; ++j) {
-      const int q = __builtin_amdgcn_readlane(pos, j);
-      if (q < 0) continue;
-      T* dst = xp + (int64_t)q * H;
-#pragma unroll
-      for (int u = 0; u < U; ++u)
-        if (c0 + 64 * u < nv) st16(dst + (c0 + 64 * u) * V, buf[u]);
-    }
-    b0 += 64 * U;
-    if (b0 >= nv) break;
-#pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (b0 + lane + 64 * u < nv) buf[u] = ld16(src + (b0 + lane + 64 * u) * V);
   }
 }
 

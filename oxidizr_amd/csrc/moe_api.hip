@@ -558,8 +558,8 @@ void launch_router_route(hipStream_t s, int T, const D* x, const D* wr, const fl
 // Routing (from logits already in saved, unless `routed`: the fused router
 // kernel has written the routing decisions too), losses' P statistics and
 // dispatch.  With `routed` (T > kRouteSmallTokens) the dispatch stops after
-// k_scan: the caller's gather writes perm and inv_perm (k_scatter_gather16
-// from the group bases at W.gbase).
+// k_scan: the caller writes perm and inv_perm (k_scatter_groups from the
+// group bases at W.gbase).
 template <typename D>
 moe_status run_routing(moe_plan* p, hipStream_t s, int64_t T64, char* saved, char* ws,
                        const SavedLayout& L, const WsLayout& W, SideJoin* pjoin,
@@ -686,7 +686,7 @@ template <typename D>
 struct State {
   float *logits, *probs, *lse, *w, *P;
   int *idx, *counts, *offsets, *perm, *inv, *tprefix;
-  D *xp, *G, *U, *A, *Y, *sG, *sU, *sA;
+  D *G, *U, *A, *Y, *sG, *sU, *sA;
   State(char* rb, const SavedLayout& LR, char* ab, const SavedLayout& LA) {
     auto r = [&](int f) { return rb + LR.f[f]; };
     auto a = [&](int f) { return LA.fbytes[f] ? (D*)(ab + LA.f[f]) : nullptr; };
@@ -701,7 +701,6 @@ struct State {
     inv = (int*)r(MOE_SAVED_INV_PERM);
     P = (float*)r(MOE_SAVED_MEAN_PROB);
     tprefix = (int*)(rb + LR.tile_prefix);
-    xp = a(MOE_SAVED_X_PERM);
     G = a(MOE_SAVED_GATE_ACT);
     U = a(MOE_SAVED_UP_ACT);
     A = a(MOE_SAVED_SWIGLU);
@@ -828,7 +827,7 @@ void with_row_tiling(const int* offsets, const int* tprefix_all, int E, int64_t 
 // needs none).  The GEMMs read each assignment's token row of x through the
 // permutation (no permuted copy of x).  `timed`: record the stages.
 // `gbase` (not null): the dispatch stopped after k_scan over the fused
-// router's 16-token groups, whose bases gbase holds; k_scatter_gather16
+// router's 16-token groups, whose bases gbase holds; k_scatter_groups
 // then writes perm and inv_perm.
 template <typename D>
 moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State<D>& st,
@@ -843,8 +842,8 @@ moe_status routed_fwd(moe_plan* p, hipStream_t s, int T, const D* x, const State
   const bool skinny = std::is_same<D, bf16_t>::value && T <= kSkinnyMaxTokens;
   if (gbase) {  // the dispatch's last launch
     StageTimer tm(p, s, stage(MOE_STAGE_DISPATCH));
-    hipLaunchKernelGGL(k_scatter_gather16<D>, dim3(ceil_div(T, 4)), dim3(256), 0, s, x, st.idx,
-                       T, k, E, H, gbase, st.perm, st.inv, (D*)nullptr);
+    hipLaunchKernelGGL(k_scatter_groups, dim3(ceil_div(T, 4)), dim3(256), 0, s, st.idx, T, k, E,
+                       gbase, st.perm, st.inv);
     LAUNCH_CHECK();
   }
   const bf16_t* xsrc = (const bf16_t*)x;
@@ -999,7 +998,7 @@ moe_status forward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* x,
     LAUNCH_CHECK();
   }
   // the fused router's dispatch stops after k_scan; the routed forward's
-  // first launch (k_scatter_gather16, scatter only) writes perm and inv_perm
+  // first launch (k_scatter_groups) writes perm and inv_perm
   const bool defer = fused;
   moe_status r = run_routing<D>(p, s, T64, rb, ws, LR, W, &p_join, fused);
   if (r != MOE_OK) return r;
@@ -1147,7 +1146,7 @@ moe_status backward_impl(moe_plan* p, hipStream_t s, int64_t T64, const D* dout,
   }
   float* dwp = (float*)(ws + W.dwp);
   // From here the routed weight gradients run on the weight-gradient stream
-  // ws2 (they read dY, A, X_perm and, after the down projection's input
+  // ws2 (they read dY, A, the weighted token rows and, after the down projection's input
   // gradient, dG / dU); the input gradients and the router backward on s.
   const hipStream_t ws2 = p->wgrad_stream(s);
   HIP_TRY(wgrad_join.fork(s, ws2, p->wfork, p->wjoin));
