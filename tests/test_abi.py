@@ -216,3 +216,12 @@ def test_workspace_check_refuses_bad_input():
     good = _cfg(64, 4, 2, 32, 0, True)
     assert L.moe_workspace_check(ctypes.byref(good), -5) == 1
     assert L.moe_workspace_check(ctypes.byref(good), (1 << 24) + 1) == 4
+
+
+def test_missing_library_fails_loudly(tmp_path, monkeypatch):
+    """With no built libmoe_hip.so there is no CPU fallback: loading raises and
+    names the build step."""
+    monkeypatch.setattr(_lib, "_lib", None)
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "libmoe_hip.so"))
+    with pytest.raises(RuntimeError, match="is missing: build it"):
+        _lib.load()
